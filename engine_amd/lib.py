@@ -1,0 +1,86 @@
+"""ctypes bindings for the hip backend's C ABI (include/lykuro_hip.h and
+include/lykuro_hip_model.h).
+
+The libraries are built in-tree by engine_amd/build.py. Loading fails loudly
+when they are missing: there is no CPU or PyTorch fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+KERNEL_LIB = os.path.join(PKG, "liblykuro_hip.so")
+MODEL_LIB = os.path.join(PKG, "liblykuro_hip_model.so")
+HEADERS = [os.path.join(ROOT, "include", "lykuro_hip.h"),
+           os.path.join(ROOT, "include", "lykuro_hip_model.h")]
+
+P, I, I64, U16, U32, U64, F = (C.c_void_p, C.c_int, C.c_int64, C.c_uint16, C.c_uint32,
+                               C.c_uint64, C.c_float)
+
+STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported shape", 3: "workspace too small",
+          4: "kernel launch failed", 5: "HIP runtime error"}
+
+EPI_STORE, EPI_ADD, EPI_STORE_F16, EPI_SILU_F16 = 0, 1, 2, 3
+
+
+class LykError(RuntimeError):
+    def __init__(self, fn, code):
+        super().__init__(f"{fn} failed: {STATUS.get(code, code)} ({code})")
+        self.code = code
+
+
+_KERNEL_SIGS = {
+    "lyk_abi_version": (I, []),
+    "lyk_q4_layout": (I, [I64, I64, I, C.POINTER(U64), C.POINTER(U64)]),
+    "lyk_q8_layout": (I, [I64, I64, I, C.POINTER(U64), C.POINTER(U64)]),
+    "lyk_q4_quantize": (I, [P, I64, I64, P, P]),
+    "lyk_q8_quantize": (I, [P, I64, I64, P, P]),
+    "lyk_q4_pack": (I, [P, P, P, P, I64, I64, P, P]),
+    "lyk_q8_pack": (I, [P, P, P, P, I64, I64, P, P]),
+    "lyk_hip_q4_unpack": (I, [P, P, I64, I64, I, P, P, P]),
+    "lyk_hip_q8_unpack": (I, [P, P, I64, I64, I, P, P, P]),
+    "lyk_hip_q4_dequant": (I, [P, P, I64, I64, I, P, P]),
+    "lyk_hip_q8_dequant": (I, [P, P, I64, I64, I, P, P]),
+    "lyk_hip_gemv_workspace_bytes": (U64, [I64, I, I, I]),
+    "lyk_hip_gemv_splits": (I, [I64, I64, I, I, I]),
+    "lyk_hip_gemv_q4": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
+    "lyk_hip_gemv_q8": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
+}
+
+_kernels = None
+_model = None
+
+
+def _bind(lib, sigs):
+    for name, (res, args) in sigs.items():
+        f = getattr(lib, name)
+        f.restype, f.argtypes = res, args
+
+
+def kernels():
+    """The kernel library (include/lykuro_hip.h)."""
+    global _kernels
+    if _kernels is None:
+        if not os.path.exists(KERNEL_LIB):
+            raise RuntimeError(
+                f"{KERNEL_LIB} is missing: build it with `python -m engine_amd.build` "
+                "(the hip backend has no fallback path)")
+        lib = C.CDLL(KERNEL_LIB)
+        _bind(lib, _KERNEL_SIGS)
+        _kernels = lib
+    return _kernels
+
+
+def declared_symbols(header):
+    """Function names declared in one of the public headers."""
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lyk_[a-z0-9_]+)\s*\(", text)))
+
+
+def check(fn, code):
+    if code != 0:
+        raise LykError(fn, code)

@@ -1,0 +1,149 @@
+"""Torch-facing helpers over the kernel C ABI: device buffers come from
+PyTorch, every computation runs in the hip backend's own kernels."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import lib as L
+
+
+def _p(a):
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data_as(C.c_void_p)
+    if isinstance(a, torch.Tensor):
+        return C.c_void_p(a.data_ptr())
+    return a
+
+
+def stream_ptr(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def quantize(w, mode):
+    """Host load-time quantizer of the backend: (codes int8 [n,k], scales fp16 bits)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    codes = np.empty((n, k), np.int8)
+    lib = L.kernels()
+    if mode == "int4":
+        scales = np.empty((n, (k + 31) // 32), np.uint16)
+        L.check("lyk_q4_quantize", lib.lyk_q4_quantize(_p(w), n, k, _p(codes), _p(scales)))
+    elif mode == "int8":
+        scales = np.empty((n,), np.uint16)
+        L.check("lyk_q8_quantize", lib.lyk_q8_quantize(_p(w), n, k, _p(codes), _p(scales)))
+    else:
+        raise ValueError(mode)
+    return codes, scales
+
+
+def layout_bytes(n, k, mode, paired=False):
+    wb, sb = C.c_uint64(), C.c_uint64()
+    fn = L.kernels().lyk_q4_layout if mode == "int4" else L.kernels().lyk_q8_layout
+    L.check("layout", fn(n, k, int(paired), C.byref(wb), C.byref(sb)))
+    return wb.value, sb.value
+
+
+def pack(codes, scales, mode, b_codes=None, b_scales=None):
+    """Host repack into the device layout; returns (qw, qs) numpy byte arrays."""
+    n, k = codes.shape
+    wb, sb = layout_bytes(n, k, mode, b_codes is not None)
+    qw = np.empty(wb, np.uint8)
+    qs = np.empty(sb, np.uint8)
+    fn = L.kernels().lyk_q4_pack if mode == "int4" else L.kernels().lyk_q8_pack
+    rc = fn(_p(np.ascontiguousarray(codes)), _p(np.ascontiguousarray(scales)),
+            None if b_codes is None else _p(np.ascontiguousarray(b_codes)),
+            None if b_scales is None else _p(np.ascontiguousarray(b_scales)), n, k, _p(qw), _p(qs))
+    L.check("pack", rc)
+    return qw, qs
+
+
+class PackedWeight:
+    """A quantized [n, k] matrix (or an A/B pair) resident on the device."""
+
+    def __init__(self, mode, n, k, qw, qs, paired=False, device="cuda"):
+        self.mode, self.n, self.k, self.paired = mode, n, k, paired
+        self.qw = torch.from_numpy(qw).to(device)
+        self.qs = torch.from_numpy(qs).to(device)
+
+    @classmethod
+    def from_codes(cls, mode, codes, scales, b_codes=None, b_scales=None, device="cuda"):
+        qw, qs = pack(codes, scales, mode, b_codes, b_scales)
+        n, k = codes.shape
+        return cls(mode, n, k, qw, qs, b_codes is not None, device)
+
+    @classmethod
+    def from_float(cls, mode, w, b=None, device="cuda"):
+        codes, scales = quantize(w, mode)
+        bc = bs = None
+        if b is not None:
+            bc, bs = quantize(b, mode)
+        return cls.from_codes(mode, codes, scales, bc, bs, device)
+
+    @property
+    def nbytes(self):
+        return self.qw.numel() + self.qs.numel()
+
+    def unpack(self, stream=None):
+        rows = self.n * (2 if self.paired else 1)
+        codes = torch.empty((rows, self.k), dtype=torch.int8, device=self.qw.device)
+        ns = (self.k + 31) // 32 if self.mode == "int4" else 1
+        scales = torch.empty((rows, ns), dtype=torch.int16, device=self.qw.device)
+        fn = L.kernels().lyk_hip_q4_unpack if self.mode == "int4" else L.kernels().lyk_hip_q8_unpack
+        L.check("unpack", fn(_p(self.qw), _p(self.qs), self.n, self.k, int(self.paired), _p(codes),
+                             _p(scales), stream_ptr(stream)))
+        return codes, scales
+
+    def dequant(self, stream=None):
+        rows = self.n * (2 if self.paired else 1)
+        w = torch.empty((rows, self.k), dtype=torch.float32, device=self.qw.device)
+        fn = L.kernels().lyk_hip_q4_dequant if self.mode == "int4" else L.kernels().lyk_hip_q8_dequant
+        L.check("dequant", fn(_p(self.qw), _p(self.qs), self.n, self.k, int(self.paired), _p(w),
+                              stream_ptr(stream)))
+        return w
+
+
+class Workspace:
+    """Zero-initialised device scratch for split-K partials and counters."""
+
+    def __init__(self, nbytes=64 << 20, device="cuda"):
+        self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+    @property
+    def nbytes(self):
+        return self.buf.numel()
+
+
+_ws = {}
+
+
+def default_workspace(device="cuda"):
+    if device not in _ws:
+        _ws[device] = Workspace(device=device)
+    return _ws[device]
+
+
+def gemv(pw: PackedWeight, x, epilogue=L.EPI_STORE, y=None, bias=None, splits=0,
+         workspace=None, stream=None):
+    """y = W x for x fp16 [m, ldx] on the device (see lyk_hip_gemv_q4)."""
+    m, ldx = x.shape
+    assert x.dtype == torch.float16 and x.is_contiguous()
+    if y is None:
+        if epilogue == L.EPI_SILU_F16 or epilogue == L.EPI_STORE_F16:
+            y = torch.empty((m, pw.n), dtype=torch.float16, device=x.device)
+        else:
+            y = torch.empty((m, pw.n), dtype=torch.float32, device=x.device)
+    ws = workspace or default_workspace(str(x.device))
+    fn = L.kernels().lyk_hip_gemv_q4 if pw.mode == "int4" else L.kernels().lyk_hip_gemv_q8
+    rc = fn(_p(pw.qw), _p(pw.qs), pw.n, pw.k, _p(x), ldx, m, epilogue, _p(y), y.shape[1],
+            None if bias is None else _p(bias), splits, _p(ws.buf), ws.nbytes, stream_ptr(stream))
+    L.check("gemv", rc)
+    return y
+
+
+def padded_k(k, mode):
+    unit = 32 if mode == "int4" else 16
+    return (k + unit - 1) // unit * unit

@@ -1,0 +1,149 @@
+/*
+ * lykuro_hip.h -- the thin C ABI between the C++20 host model
+ * (QwenHipModel, engine_amd/csrc/host) and the hand-written gfx950 kernels of
+ * the hip backend.
+ *
+ * The reference engine has no C ABI on this path: its backend seam is the C++
+ * class GenerativeModel (model/architectures/generative_model.h:40-105) and
+ * its CUDA backend calls kernels from inside one translation unit
+ * (backends/cuda/qwen_cuda_model.cu). Each entry point below replaces one
+ * kernel family of that file; the citation names what it replaces.
+ *
+ * Conventions
+ *   - Plain pointers and sizes only. Pointers named d_* are device pointers;
+ *     `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - Every function returns 0 (LYK_OK) or a LYK_ERR_* code; nothing throws.
+ *   - No entry point allocates device memory; scratch comes from the caller's
+ *     workspace, sized by the matching *_workspace_bytes function and zeroed
+ *     by the caller once, before first use (kernels leave it zeroed again).
+ *   - fp16 values are passed as uint16_t bit patterns (IEEE binary16).
+ *   - Results are deterministic: fixed-order reductions, no float atomics.
+ */
+#ifndef LYKURO_HIP_H
+#define LYKURO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LYK_ABI_VERSION 1
+
+enum {
+    LYK_OK = 0,
+    LYK_ERR_INVALID_ARG = 1,  /* null pointer, bad size or stride */
+    LYK_ERR_SHAPE = 2,        /* shape outside what the kernel supports */
+    LYK_ERR_WORKSPACE = 3,    /* workspace too small */
+    LYK_ERR_LAUNCH = 4,       /* kernel launch failed */
+    LYK_ERR_HIP = 5,          /* other HIP runtime error */
+};
+
+/* Packed weight layouts (defined by this backend; the reference keeps plain
+ * row-major weights, qwen_cuda_model.cu:1070-1210).
+ *
+ * int4 ("q4"): symmetric, groups of 32 along K, one fp16 scale per group.
+ *   Rows are cut into tiles of 64 (one row per lane of a wave). For tile t,
+ *   group g, lane r the 16 bytes at qw[((t*Gp + g)*64 + r)*16] hold the 32
+ *   codes of row 64t+r, k = 32g..32g+31, as nibbles q+8. In each 32-bit word
+ *   w (k = 8d..8d+7 for word d) nibble j of the 8 sits at bit
+ *   {0,16,4,20,8,24,12,28}[j], so one AND/OR with 0x000F000F / 0x00F000F0
+ *   yields two fp16 values 1024+q+8 / 1024+16(q+8). Gp = groups rounded up to
+ *   a multiple of 8. Scales: qs[((t*(Gp/8) + c)*64 + r)*8 + j] is the fp16
+ *   scale of group 8c+j. Padding codes are q=0 (nibble 8).
+ * int8 ("q8"): one fp16 scale per row; tiles of 64 rows; for tile t, block b
+ *   of 16 consecutive k, lane r: 16 bytes at qw[((t*Bp + b)*64 + r)*16] hold
+ *   the codes q+128 as unsigned bytes in k order. Bp = ceil(K/16) rounded up
+ *   to a multiple of 8. Scales: qs[t*64 + r].
+ * Paired ("SiLU-gate") packing: two matrices A, B of the same shape share
+ *   tiles of 64 rows: rows 0-31 of tile t are A rows 32t.., rows 32-63 are B
+ *   rows 32t.. (A = gate_proj, B = up_proj).
+ */
+#define LYK_TILE_ROWS 64
+#define LYK_Q4_GROUP 32
+#define LYK_Q8_BLOCK 16
+
+/* Bytes of the packed weights and scales for an [n, k] matrix
+ * (paired != 0: two [n, k] matrices packed as pairs). */
+int lyk_q4_layout(int64_t n, int64_t k, int paired, uint64_t* weight_bytes,
+                  uint64_t* scale_bytes);
+int lyk_q8_layout(int64_t n, int64_t k, int paired, uint64_t* weight_bytes,
+                  uint64_t* scale_bytes);
+
+/* Host-side load-time quantizers (model/loader step; replaces
+ * WeightBuffer::Quantize, qwen_cuda_model.cu:1133-1210, with this backend's
+ * format). int4: s = fp16(absmax/7) per 32-group (1.0 for an all-zero group),
+ * q = clamp(roundf(w/s), -8, 7); int8: s = fp16(absmax/127) per row,
+ * q = clamp(roundf(w/s), -127, 127). codes row-major [n][k]; int4 scales
+ * [n][ceil(k/32)], int8 scales [n]. Multithreaded over rows. */
+int lyk_q4_quantize(const float* w, int64_t n, int64_t k, int8_t* codes,
+                    uint16_t* scales);
+int lyk_q8_quantize(const float* w, int64_t n, int64_t k, int8_t* codes,
+                    uint16_t* scales);
+
+/* Host-side repack of row-major codes/scales into the device layouts above
+ * (into host buffers of the lyk_*_layout sizes; the caller uploads them).
+ * b_codes/b_scales are the second matrix of a paired packing, else NULL. */
+int lyk_q4_pack(const int8_t* codes, const uint16_t* scales,
+                const int8_t* b_codes, const uint16_t* b_scales, int64_t n,
+                int64_t k, void* qw, void* qs);
+int lyk_q8_pack(const int8_t* codes, const uint16_t* scales,
+                const int8_t* b_codes, const uint16_t* b_scales, int64_t n,
+                int64_t k, void* qw, void* qs);
+
+/* Device-side inverse of the packing (for tests and diagnostics): writes the
+ * row-major codes and scales of the matrix (paired: the 2n rows A then B). */
+int lyk_hip_q4_unpack(const void* d_qw, const void* d_qs, int64_t n,
+                      int64_t k, int paired, int8_t* d_codes,
+                      uint16_t* d_scales, void* stream);
+int lyk_hip_q8_unpack(const void* d_qw, const void* d_qs, int64_t n,
+                      int64_t k, int paired, int8_t* d_codes,
+                      uint16_t* d_scales, void* stream);
+/* Device dequantization to row-major fp32, w = q * float(s) (exact). */
+int lyk_hip_q4_dequant(const void* d_qw, const void* d_qs, int64_t n,
+                       int64_t k, int paired, float* d_w, void* stream);
+int lyk_hip_q8_dequant(const void* d_qw, const void* d_qs, int64_t n,
+                       int64_t k, int paired, float* d_w, void* stream);
+
+/* Weight-only dequant-GEMV, y[m] = W x[m] for m < M (M = 1..4).
+ * Replaces MatVecEpi1Kernel / FusedQkv1Kernel / FusedGateUp1Kernel /
+ * MatVecBatchKernel / MatVecEpilogueKernel (qwen_cuda_model.cu:533-578,
+ * 615-819, 1268-1378) and the CPU MatVec (qwen_model.cpp:21-31).
+ *   x: fp16 [M][ldx], ldx >= k rounded up to 32 (q4) or 16 (q8); entries
+ *      between k and that bound must be 0.
+ *   epilogue (per output row r of batch row m):
+ *     LYK_EPI_STORE     y fp32 [M][ldy]: y = Wx (+ bias[r] when bias != NULL)
+ *     LYK_EPI_ADD       y fp32 [M][ldy]: y += Wx   (residual add)
+ *     LYK_EPI_STORE_F16 y fp16 [M][ldy]: y = fp16(Wx (+ bias))
+ *     LYK_EPI_SILU_F16  paired packing; y fp16 [M][ldy]:
+ *                       y = fp16(silu(A x) * (B x)), silu(g) = g/(1+exp(-g))
+ *   splits: 0 = choose; else the number of workgroups sharing one row tile's
+ *           K range (partials merged in fixed order by the last one).
+ *   workspace: lyk_hip_gemv_workspace_bytes(n, M, splits, paired) bytes,
+ *              zeroed once before first use. */
+enum {
+    LYK_EPI_STORE = 0,
+    LYK_EPI_ADD = 1,
+    LYK_EPI_STORE_F16 = 2,
+    LYK_EPI_SILU_F16 = 3,
+};
+uint64_t lyk_hip_gemv_workspace_bytes(int64_t n, int m, int splits,
+                                      int paired);
+int lyk_hip_gemv_splits(int64_t n, int64_t k, int m, int paired, int q8);
+int lyk_hip_gemv_q4(const void* d_qw, const void* d_qs, int64_t n, int64_t k,
+                    const uint16_t* d_x, int64_t ldx, int m, int epilogue,
+                    void* d_y, int64_t ldy, const float* d_bias, int splits,
+                    void* d_workspace, uint64_t workspace_bytes, void* stream);
+int lyk_hip_gemv_q8(const void* d_qw, const void* d_qs, int64_t n, int64_t k,
+                    const uint16_t* d_x, int64_t ldx, int m, int epilogue,
+                    void* d_y, int64_t ldy, const float* d_bias, int splits,
+                    void* d_workspace, uint64_t workspace_bytes, void* stream);
+
+int lyk_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LYKURO_HIP_H */
