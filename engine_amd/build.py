@@ -39,6 +39,7 @@ HIP_FLAGS = ["-O3", "-std=c++20", "-fPIC", f"--offload-arch={ARCH}",
 # rounding bit for bit).
 CXX_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra",
              "-Wno-unused-parameter", "-I", INCLUDE, "-I", os.path.join(CSRC, "host"),
+             "-I", os.path.join(CSRC, "host", "iface"),
              "-I", os.path.join(ROCM, "include"), "-D__HIP_PLATFORM_AMD__"]
 
 KERNEL_HOST_SOURCES = ["quant_pack.cpp"]  # C-ABI host helpers in the kernel lib

@@ -1,0 +1,955 @@
+// QwenHipModel: host side of the MI355X hip backend (C++20). Owns device
+// memory, the paged KV pool and the decode step; every device computation is
+// a call into the gfx950 kernel library through include/lykuro_hip.h.
+//
+// Contract followed (reference paths): GenerativeModel
+// (model/architectures/generative_model.h:40-105); error semantics of
+// QwenModel / QwenCudaModel Prefill, Decode, DecodeBatch and GreedyRun
+// (model/architectures/qwen/qwen_model.cpp:333-412,
+// backends/cuda/qwen_cuda_model.cu:2518-2660, 2641-2776, 2778-3102); paged
+// pool and prefix cache (qwen_cuda_model.cu:1623-1749, 1913-2008,
+// 2545-2608).
+#include "qwen_hip_model.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <thread>
+#include <unordered_map>
+
+#include "fp16.h"
+#include "lykuro_hip.h"
+#include "lykuro_hip_model.h"
+
+namespace lykuro::nie {
+
+namespace {
+
+constexpr const char kComponent[] = "qwen_hip";
+constexpr int kMaxBatch = 4;          // rows per GEMV pass (lyk_hip_gemv_* limit)
+constexpr uint32_t kGreedyMax = 256;  // greedy steps per GreedyRun call
+
+Status HipFail(hipError_t err, const char* what) {
+    if (err == hipErrorOutOfMemory || err == hipErrorMemoryAllocation)
+        return Status(ErrorCode::kGpuOom, what, kComponent);
+    return Status(ErrorCode::kGpuUnhealthy, what, kComponent);
+}
+
+Status KernelFail(int rc, const char* what) {
+    if (rc == LYK_ERR_SHAPE) return Status(ErrorCode::kUnsupportedModel, what, kComponent);
+    return Status(ErrorCode::kGpuUnhealthy, what, kComponent).WithDetail("lyk_status", rc);
+}
+
+#define HIP_OK(expr, what)                                \
+    do {                                                  \
+        hipError_t e_ = (expr);                           \
+        if (e_ != hipSuccess) return HipFail(e_, what);   \
+    } while (0)
+
+#define LYK_OK_OR(expr, what)                          \
+    do {                                               \
+        int rc_ = (expr);                              \
+        if (rc_ != LYK_OK) return KernelFail(rc_, what); \
+    } while (0)
+
+int64_t RoundUp(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) {
+        o.p = nullptr;
+        o.bytes = 0;
+    }
+    DevBuf& operator=(DevBuf&& o) noexcept {
+        if (this != &o) {
+            Free();
+            p = o.p;
+            bytes = o.bytes;
+            o.p = nullptr;
+            o.bytes = 0;
+        }
+        return *this;
+    }
+    ~DevBuf() { Free(); }
+    void Free() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    Status Alloc(size_t n, bool zero = true) {
+        Free();
+        HIP_OK(hipMalloc(&p, n ? n : 1), "device allocation failed");
+        bytes = n;
+        if (zero) HIP_OK(hipMemset(p, 0, n ? n : 1), "device memset failed");
+        return Status::Ok();
+    }
+    Status Upload(const void* src, size_t n) {
+        Status s = Alloc(n, false);
+        if (!s.ok()) return s;
+        HIP_OK(hipMemcpy(p, src, n, hipMemcpyHostToDevice), "weight upload failed");
+        return Status::Ok();
+    }
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+struct PinnedBuf {
+    void* p = nullptr;
+    ~PinnedBuf() {
+        if (p) (void)hipHostFree(p);
+    }
+    Status Alloc(size_t n) {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        HIP_OK(hipHostMalloc(&p, n ? n : 1, hipHostMallocDefault), "pinned allocation failed");
+        return Status::Ok();
+    }
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+struct PackedMat {
+    DevBuf qw, qs;
+    int64_t n = 0, k = 0;
+    bool paired = false;
+};
+
+// FNV-1a 64, the prefix-cache chain hash (qwen_cuda_model.cu:1623-1630).
+uint64_t Fnv64(uint64_t h, const void* data, size_t len) {
+    const uint8_t* p = static_cast<const uint8_t*>(data);
+    for (size_t i = 0; i < len; ++i) {
+        h ^= p[i];
+        h *= 1099511628211ULL;
+    }
+    return h;
+}
+
+// Block pool shared by every sequence of the model: refcounted blocks, a
+// free list, and prefix-cached blocks that stay resident (evictable, LRU)
+// after their last user releases them. Block ids index every layer's pool.
+class KvPool {
+public:
+    void Init(uint32_t num_blocks, uint32_t block_tokens) {
+        block_tokens_ = block_tokens;
+        meta_.assign(num_blocks, Meta{});
+        free_.clear();
+        for (uint32_t b = 0; b < num_blocks; ++b) free_.push_back(int(num_blocks - 1 - b));
+        by_hash_.clear();
+    }
+    uint32_t block_tokens() const { return block_tokens_; }
+    uint32_t num_blocks() const { return uint32_t(meta_.size()); }
+    uint32_t free_blocks() const {
+        uint32_t evictable = 0;
+        for (const Meta& m : meta_) evictable += (m.cached && m.refs == 0);
+        return uint32_t(free_.size()) + evictable;
+    }
+    bool Allocate(int& out) {
+        if (!free_.empty()) {
+            out = free_.back();
+            free_.pop_back();
+            meta_[out] = Meta{};
+            meta_[out].refs = 1;
+            return true;
+        }
+        int victim = -1;
+        uint64_t oldest = UINT64_MAX;
+        for (uint32_t b = 0; b < meta_.size(); ++b)
+            if (meta_[b].cached && meta_[b].refs == 0 && meta_[b].tick < oldest) {
+                oldest = meta_[b].tick;
+                victim = int(b);
+            }
+        if (victim < 0) return false;
+        by_hash_.erase(meta_[victim].hash);
+        meta_[victim] = Meta{};
+        meta_[victim].refs = 1;
+        out = victim;
+        return true;
+    }
+    void Release(int b) {
+        Meta& m = meta_[b];
+        if (m.refs > 0) --m.refs;
+        if (m.refs == 0) {
+            if (m.cached) m.tick = ++tick_;
+            else free_.push_back(b);
+        }
+    }
+    bool Lookup(uint64_t hash, int& out) {
+        auto it = by_hash_.find(hash);
+        if (it == by_hash_.end()) return false;
+        out = it->second;
+        ++meta_[out].refs;
+        meta_[out].tick = ++tick_;
+        return true;
+    }
+    void Register(uint64_t hash, int b) {
+        if (by_hash_.count(hash) || meta_[b].cached) return;  // first writer wins
+        meta_[b].cached = true;
+        meta_[b].hash = hash;
+        meta_[b].tick = ++tick_;
+        by_hash_.emplace(hash, b);
+    }
+
+private:
+    struct Meta {
+        int refs = 0;
+        bool cached = false;
+        uint64_t hash = 0;
+        uint64_t tick = 0;
+    };
+    uint32_t block_tokens_ = 16;
+    std::vector<Meta> meta_;
+    std::vector<int> free_;
+    std::unordered_map<uint64_t, int> by_hash_;
+    uint64_t tick_ = 0;
+};
+
+class HipSequenceState final : public SequenceState {
+public:
+    HipSequenceState(KvPool* pool, uint32_t max_tokens, SequenceOptions options)
+        : pool_(pool), max_tokens_(max_tokens), options_(std::move(options)) {}
+    ~HipSequenceState() override {
+        for (int b : blocks_) pool_->Release(b);
+    }
+    uint32_t length() const override { return length_; }
+    uint32_t capacity() const override { return max_tokens_; }
+    const SequenceOptions& options() const { return options_; }
+    const std::vector<int>& blocks() const { return blocks_; }
+
+    // Blocks for positions [0, pos]; capacity_exhausted when the pool is dry.
+    Status EnsureBlocks(uint32_t pos) {
+        const uint32_t need = pos / pool_->block_tokens() + 1;
+        while (blocks_.size() < need) {
+            int b = -1;
+            if (!pool_->Allocate(b))
+                return Status(ErrorCode::kCapacityExhausted, "kv block pool exhausted", kComponent);
+            blocks_.push_back(b);
+        }
+        return Status::Ok();
+    }
+    void AttachPrefix(std::vector<int> shared, uint32_t tokens) {
+        blocks_ = std::move(shared);
+        length_ = tokens;
+    }
+    void Advance(uint32_t n = 1) { length_ += n; }
+
+private:
+    KvPool* pool_;
+    uint32_t max_tokens_;
+    uint32_t length_ = 0;
+    SequenceOptions options_;
+    std::vector<int> blocks_;
+};
+
+enum class StepMode { kHidden, kLogits, kGreedy };
+
+// Tensor kinds of the synthetic generator's stream ids (kind*1000 + layer).
+enum Kind {
+    kEmbed = 0, kInputNorm, kQW, kQB, kKW, kKB, kVW, kVB, kOW, kPostNorm, kGateW, kUpW, kDownW,
+    kFinalNorm, kLmHead
+};
+
+std::string LayerName(uint32_t l, const char* suffix) {
+    return "model.layers." + std::to_string(l) + "." + suffix;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ weight sources
+
+Status SafetensorsWeightSource::Read(const std::string& name, const std::vector<uint64_t>& shape,
+                                     std::vector<float>& out) const {
+    const TensorInfo* info = file_.FindTensor(name);
+    const uint8_t* data = file_.TensorData(name);
+    if (info == nullptr || data == nullptr)
+        return Status(ErrorCode::kArtifactVerificationFailed, "expected weight tensor missing", kComponent);
+    if (info->shape != shape)
+        return Status(ErrorCode::kArtifactVerificationFailed, "weight tensor shape mismatch", kComponent);
+    out.resize(info->element_count);
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(data);
+    switch (info->dtype) {
+        case Dtype::kF32: std::memcpy(out.data(), data, info->data_size); break;
+        case Dtype::kF16:
+            for (uint64_t i = 0; i < info->element_count; ++i) out[i] = lyk::f16_to_f32(h[i]);
+            break;
+        case Dtype::kBf16:
+            for (uint64_t i = 0; i < info->element_count; ++i) out[i] = lyk::bf16_to_f32(h[i]);
+            break;
+    }
+    return Status::Ok();
+}
+
+Status SyntheticWeightSource::Read(const std::string& name, const std::vector<uint64_t>& shape,
+                                   std::vector<float>& out) const {
+    uint64_t count = 1;
+    for (uint64_t d : shape) count *= d;
+    out.resize(count);
+    if (name.find("norm") != std::string::npos) {
+        std::fill(out.begin(), out.end(), 1.0f);
+        return Status::Ok();
+    }
+    int kind = -1;
+    uint32_t layer = 0;
+    if (name == "model.embed_tokens.weight") kind = kEmbed;
+    else if (name == "lm_head.weight") kind = kLmHead;
+    else {
+        static const std::pair<const char*, int> kLayer[] = {
+            {"self_attn.q_proj.weight", kQW}, {"self_attn.q_proj.bias", kQB},
+            {"self_attn.k_proj.weight", kKW}, {"self_attn.k_proj.bias", kKB},
+            {"self_attn.v_proj.weight", kVW}, {"self_attn.v_proj.bias", kVB},
+            {"self_attn.o_proj.weight", kOW}, {"mlp.gate_proj.weight", kGateW},
+            {"mlp.up_proj.weight", kUpW},     {"mlp.down_proj.weight", kDownW}};
+        const std::string prefix = "model.layers.";
+        if (name.rfind(prefix, 0) == 0) {
+            const size_t dot = name.find('.', prefix.size());
+            layer = uint32_t(std::stoul(name.substr(prefix.size(), dot - prefix.size())));
+            const std::string suffix = name.substr(dot + 1);
+            for (const auto& [s, k] : kLayer)
+                if (suffix == s) kind = k;
+        }
+    }
+    if (kind < 0)
+        return Status(ErrorCode::kArtifactVerificationFailed, "expected weight tensor missing", kComponent);
+    const uint64_t stream = uint64_t(kind) * 1000 + layer;
+    const unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    const uint64_t workers = count < (1u << 20) ? 1 : hw;
+    std::vector<std::thread> pool;
+    for (uint64_t t = 1; t < workers; ++t) {
+        const uint64_t a = count * t / workers, b = count * (t + 1) / workers;
+        pool.emplace_back([this, stream, a, b, &out] { lyk_synth_normal(seed_, stream, a, b - a, sigma_, out.data() + a); });
+    }
+    lyk_synth_normal(seed_, stream, 0, count / workers, sigma_, out.data());
+    for (auto& th : pool) th.join();
+    return Status::Ok();
+}
+
+// ------------------------------------------------------------------- config
+
+Status HipQwenConfig::FromManifest(const ModelManifest& m, HipQwenConfig& out) {
+    auto fail = [](const char* msg) {
+        return Status(ErrorCode::kArtifactVerificationFailed, msg, kComponent);
+    };
+    out.vocab_size = m.vocab_size;
+    out.hidden_size = m.hidden_size;
+    out.num_layers = m.num_layers;
+    out.num_heads = m.num_attention_heads;
+    out.num_kv_heads = m.num_key_value_heads;
+    out.head_dim = m.head_dim;
+    out.intermediate_size = m.intermediate_size;
+    out.max_context_tokens = m.max_context_tokens;
+    out.rms_norm_eps = m.rms_norm_eps > 0 ? float(m.rms_norm_eps) : 1e-6f;
+    out.rope_theta = m.rope_theta > 0 ? float(m.rope_theta) : 10000.0f;
+    out.tie_word_embeddings = m.tie_word_embeddings;
+    out.eos_token_ids = m.eos_token_ids;
+    if (out.intermediate_size == 0) return fail("manifest missing intermediate_size");
+    if (out.head_dim % 2 != 0) return fail("head_dim must be even for RoPE");
+    if (out.num_kv_heads == 0 || out.num_heads % out.num_kv_heads != 0)
+        return fail("attention head configuration inconsistent");
+    if (out.eos_token_ids.empty()) return fail("manifest missing eos_token_ids");
+    for (uint32_t id : out.eos_token_ids)
+        if (id >= out.vocab_size) return fail("eos token id out of vocab range");
+    return Status::Ok();
+}
+
+// --------------------------------------------------------------------- impl
+
+struct QwenHipModel::Impl {
+    struct Layer {
+        DevBuf input_norm, post_norm, qkv_bias;
+        PackedMat qkv, o, gateup, down;
+    };
+
+    HipModelOptions opt;
+    HipQwenConfig c;
+    hipStream_t stream = nullptr;
+    bool q8 = false;
+
+    DevBuf embed, final_norm;
+    PackedMat lm_head;
+    std::vector<Layer> layers;
+
+    KvPool pool;
+    DevBuf kv;  // [layer][K|V][num_blocks][nkv][bt][hd] fp16
+    size_t kv_layer_elems = 0;
+
+    DevBuf rcos, rsin;
+    uint32_t rope_cap = 0, table_stride = 0;
+
+    // decode-step buffers (kMaxBatch rows)
+    int64_t ldx_h = 0, ldx_q = 0, ldx_i = 0, qkv_n = 0;
+    DevBuf d_tokens, d_pos, d_tables, d_h, d_xn, d_attn, d_act, d_qkv, d_q, d_logits, d_ws,
+        d_history, d_step, d_nonfinite;
+    PinnedBuf h_tokens, h_pos, h_tables, h_logits, h_history, h_nonfinite;
+    uint64_t ws_bytes = 0;
+
+    std::map<uint64_t, hipGraphExec_t> graphs;
+    uint64_t prefix_hits = 0;
+    uint64_t gemv_bytes = 0;
+
+    ~Impl() {
+        for (auto& [k, g] : graphs) (void)hipGraphExecDestroy(g);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    uint16_t* kcache(uint32_t l) const { return kv.as<uint16_t>() + (size_t)l * 2 * kv_layer_elems; }
+    uint16_t* vcache(uint32_t l) const { return kcache(l) + kv_layer_elems; }
+
+    void DropGraphs() {
+        for (auto& [k, g] : graphs) (void)hipGraphExecDestroy(g);
+        graphs.clear();
+    }
+
+    // cos/sin tables and block-table stride for positions < cap; rebuilt
+    // (and cached graphs dropped) when a longer sequence is created.
+    Status EnsureRope(uint32_t cap) {
+        if (cap <= rope_cap) return Status::Ok();
+        const uint32_t half = c.head_dim / 2;
+        std::vector<float> cs((size_t)cap * half), sn((size_t)cap * half);
+        for (uint32_t i = 0; i < half; ++i) {
+            // the CPU reference's expressions (qwen_model.cpp:45-48), in float
+            const float freq = std::pow(c.rope_theta, -2.0f * float(i) / float(c.head_dim));
+            for (uint32_t p = 0; p < cap; ++p) {
+                const float angle = float(p) * freq;
+                cs[(size_t)p * half + i] = std::cos(angle);
+                sn[(size_t)p * half + i] = std::sin(angle);
+            }
+        }
+        HIP_OK(hipStreamSynchronize(stream), "device execution failed");
+        DropGraphs();
+        Status s = rcos.Upload(cs.data(), cs.size() * 4);
+        if (!s.ok()) return s;
+        s = rsin.Upload(sn.data(), sn.size() * 4);
+        if (!s.ok()) return s;
+        rope_cap = cap;
+        table_stride = std::max<uint32_t>(1, (cap + pool.block_tokens() - 1) / pool.block_tokens());
+        s = d_tables.Alloc((size_t)kMaxBatch * table_stride * 4);
+        if (!s.ok()) return s;
+        return h_tables.Alloc((size_t)kMaxBatch * table_stride * 4);
+    }
+
+    Status Gemv(const PackedMat& w, const uint16_t* x, int64_t ldx, int m, int epi, void* y,
+                int64_t ldy, const float* bias) {
+        const int rc = q8 ? lyk_hip_gemv_q8(w.qw.p, w.qs.p, w.n, w.k, x, ldx, m, epi, y, ldy, bias, 0,
+                                            d_ws.p, ws_bytes, stream)
+                          : lyk_hip_gemv_q4(w.qw.p, w.qs.p, w.n, w.k, x, ldx, m, epi, y, ldy, bias, 0,
+                                            d_ws.p, ws_bytes, stream);
+        LYK_OK_OR(rc, "gemv launch failed");
+        return Status::Ok();
+    }
+
+    static int SplitsFor(uint32_t max_ctx) {
+        if (max_ctx <= 128) return 1;
+        if (max_ctx <= 1024) return 8;
+        if (max_ctx <= 4096) return 16;
+        return 32;
+    }
+
+    // The decode step for rows 0..m-1 whose token, position and block table
+    // are already on the device.
+    Status LaunchStep(int m, int splits, StepMode mode) {
+        const int H = int(c.hidden_size), nq = int(c.num_heads), nkv = int(c.num_kv_heads),
+                  hd = int(c.head_dim);
+        const float eps = c.rms_norm_eps;
+        LYK_OK_OR(lyk_hip_embed_rmsnorm(embed.as<float>(), c.vocab_size, d_tokens.as<int32_t>(), m, H,
+                                        d_h.as<float>(), H, layers[0].input_norm.as<float>(), eps,
+                                        d_xn.as<uint16_t>(), ldx_h, stream),
+                  "embedding launch failed");
+        for (uint32_t l = 0; l < c.num_layers; ++l) {
+            Layer& L = layers[l];
+            Status s = Gemv(L.qkv, d_xn.as<uint16_t>(), ldx_h, m, LYK_EPI_STORE, d_qkv.p, qkv_n,
+                            L.qkv_bias.as<float>());
+            if (!s.ok()) return s;
+            LYK_OK_OR(lyk_hip_rope_kv_append(d_qkv.as<float>(), qkv_n, m, nq, nkv, hd, d_pos.as<int32_t>(),
+                                             rcos.as<float>(), rsin.as<float>(), int(rope_cap),
+                                             d_q.as<float>(), kcache(l), vcache(l), d_tables.as<int32_t>(),
+                                             int(table_stride), int(pool.block_tokens()),
+                                             int(pool.num_blocks()), stream),
+                      "rope launch failed");
+            LYK_OK_OR(lyk_hip_attn_decode(d_q.as<float>(), kcache(l), vcache(l), d_tables.as<int32_t>(),
+                                          int(table_stride), d_pos.as<int32_t>(), m, nq, nkv, hd,
+                                          int(pool.block_tokens()), int(pool.num_blocks()), splits,
+                                          d_attn.as<uint16_t>(), ldx_q, d_ws.p, ws_bytes, stream),
+                      "attention launch failed");
+            s = Gemv(L.o, d_attn.as<uint16_t>(), ldx_q, m, LYK_EPI_ADD, d_h.p, H, nullptr);
+            if (!s.ok()) return s;
+            LYK_OK_OR(lyk_hip_rmsnorm_f16(d_h.as<float>(), H, L.post_norm.as<float>(), eps, m, H,
+                                          d_xn.as<uint16_t>(), ldx_h, stream),
+                      "rmsnorm launch failed");
+            s = Gemv(L.gateup, d_xn.as<uint16_t>(), ldx_h, m, LYK_EPI_SILU_F16, d_act.p, ldx_i, nullptr);
+            if (!s.ok()) return s;
+            s = Gemv(L.down, d_act.as<uint16_t>(), ldx_i, m, LYK_EPI_ADD, d_h.p, H, nullptr);
+            if (!s.ok()) return s;
+            const float* next_norm =
+                l + 1 < c.num_layers ? layers[l + 1].input_norm.as<float>() : final_norm.as<float>();
+            LYK_OK_OR(lyk_hip_rmsnorm_f16(d_h.as<float>(), H, next_norm, eps, m, H, d_xn.as<uint16_t>(),
+                                          ldx_h, stream),
+                      "rmsnorm launch failed");
+        }
+        if (mode == StepMode::kHidden) return Status::Ok();
+        Status s = Gemv(lm_head, d_xn.as<uint16_t>(), ldx_h, m, LYK_EPI_STORE, d_logits.p, c.vocab_size,
+                        nullptr);
+        if (!s.ok()) return s;
+        if (mode == StepMode::kGreedy)
+            LYK_OK_OR(lyk_hip_argmax(d_logits.as<float>(), c.vocab_size, 1, c.vocab_size,
+                                     d_tokens.as<int32_t>(), d_nonfinite.as<int32_t>(), d_pos.as<int32_t>(),
+                                     d_history.as<int32_t>(), d_step.as<int32_t>(), d_ws.p, ws_bytes,
+                                     stream),
+                      "argmax launch failed");
+        return Status::Ok();
+    }
+
+    // Runs one step, through a cached HIP graph when enabled.
+    Status RunStep(int m, int splits, StepMode mode) {
+        if (!opt.use_graphs) return LaunchStep(m, splits, mode);
+        const uint64_t key = (uint64_t(m) << 32) | (uint64_t(splits) << 8) | uint64_t(mode);
+        auto it = graphs.find(key);
+        if (it == graphs.end()) {
+            HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "graph capture failed");
+            Status s = LaunchStep(m, splits, mode);
+            hipGraph_t g = nullptr;
+            const hipError_t e = hipStreamEndCapture(stream, &g);
+            if (!s.ok()) {
+                if (g) (void)hipGraphDestroy(g);
+                return s;
+            }
+            if (e != hipSuccess) return HipFail(e, "graph capture failed");
+            hipGraphExec_t exec = nullptr;
+            const hipError_t ie = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (ie != hipSuccess) return HipFail(ie, "graph instantiation failed");
+            it = graphs.emplace(key, exec).first;
+        }
+        HIP_OK(hipGraphLaunch(it->second, stream), "graph launch failed");
+        return Status::Ok();
+    }
+
+    // Uploads tokens, positions and block tables of up to kMaxBatch rows.
+    Status UploadRows(const std::vector<HipSequenceState*>& seqs, const std::vector<uint32_t>& tokens,
+                      const std::vector<uint32_t>& positions) {
+        const size_t m = seqs.size();
+        int32_t* ht = h_tokens.as<int32_t>();
+        int32_t* hp = h_pos.as<int32_t>();
+        int32_t* tb = h_tables.as<int32_t>();
+        for (size_t i = 0; i < m; ++i) {
+            ht[i] = int32_t(tokens[i]);
+            hp[i] = int32_t(positions[i]);
+            const auto& blocks = seqs[i]->blocks();
+            std::copy(blocks.begin(), blocks.end(), tb + i * table_stride);
+        }
+        HIP_OK(hipMemcpyAsync(d_tokens.p, ht, m * 4, hipMemcpyHostToDevice, stream), "token upload failed");
+        HIP_OK(hipMemcpyAsync(d_pos.p, hp, m * 4, hipMemcpyHostToDevice, stream), "position upload failed");
+        HIP_OK(hipMemcpyAsync(d_tables.p, tb, m * table_stride * 4, hipMemcpyHostToDevice, stream),
+               "block table upload failed");
+        return Status::Ok();
+    }
+};
+
+// --------------------------------------------------------------------- load
+
+namespace {
+
+Status QuantizeUpload(bool q8, const std::vector<float>& a, const std::vector<float>* b, int64_t n,
+                      int64_t k, PackedMat& out, uint64_t& bytes) {
+    const int64_t ns = q8 ? 1 : (k + 31) / 32;
+    std::vector<int8_t> ca((size_t)(n * k)), cb;
+    std::vector<uint16_t> sa((size_t)(n * ns)), sb;
+    int rc = q8 ? lyk_q8_quantize(a.data(), n, k, ca.data(), sa.data())
+                : lyk_q4_quantize(a.data(), n, k, ca.data(), sa.data());
+    if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight quantization failed", kComponent);
+    if (b) {
+        cb.resize(ca.size());
+        sb.resize(sa.size());
+        rc = q8 ? lyk_q8_quantize(b->data(), n, k, cb.data(), sb.data())
+                : lyk_q4_quantize(b->data(), n, k, cb.data(), sb.data());
+        if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight quantization failed", kComponent);
+    }
+    uint64_t wb = 0, sbytes = 0;
+    rc = q8 ? lyk_q8_layout(n, k, b != nullptr, &wb, &sbytes) : lyk_q4_layout(n, k, b != nullptr, &wb, &sbytes);
+    if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight shape unsupported", kComponent);
+    std::vector<uint8_t> qw(wb), qs(sbytes);
+    rc = q8 ? lyk_q8_pack(ca.data(), sa.data(), b ? cb.data() : nullptr, b ? sb.data() : nullptr, n, k,
+                          qw.data(), qs.data())
+            : lyk_q4_pack(ca.data(), sa.data(), b ? cb.data() : nullptr, b ? sb.data() : nullptr, n, k,
+                          qw.data(), qs.data());
+    if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight packing failed", kComponent);
+    Status s = out.qw.Upload(qw.data(), qw.size());
+    if (!s.ok()) return s;
+    s = out.qs.Upload(qs.data(), qs.size());
+    if (!s.ok()) return s;
+    out.n = n;
+    out.k = k;
+    out.paired = b != nullptr;
+    bytes += wb + sbytes;
+    return Status::Ok();
+}
+
+Status UploadF32(const std::vector<float>& v, DevBuf& out) { return out.Upload(v.data(), v.size() * 4); }
+
+}  // namespace
+
+QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const SafetensorsFile& weights,
+                                            const HipModelOptions& options) {
+    SafetensorsWeightSource src(weights);
+    return Load(manifest, src, options);
+}
+
+QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const WeightSource& src,
+                                            const HipModelOptions& options) {
+    LoadResult r;
+    std::unique_ptr<QwenHipModel> model(new QwenHipModel());
+    r.status = HipQwenConfig::FromManifest(manifest, model->config_);
+    if (!r.status.ok()) return r;
+    const HipQwenConfig& c = model->config_;
+    model->limits_.vocab_size = c.vocab_size;
+    model->limits_.max_context_tokens = c.max_context_tokens;
+    model->limits_.eos_token_ids = c.eos_token_ids;
+    model->device_id_ = options.device_id;
+    if (options.kv_block_tokens == 0 || c.head_dim > 512 || c.num_heads / c.num_kv_heads > 16 ||
+        (c.num_heads / c.num_kv_heads) * c.head_dim > 4096) {
+        r.status = Status(ErrorCode::kUnsupportedModel, "model geometry unsupported by the hip kernels",
+                          kComponent);
+        return r;
+    }
+
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || options.device_id < 0 || options.device_id >= devices) {
+        r.status = Status(ErrorCode::kGpuUnhealthy, "hip device not available", kComponent);
+        return r;
+    }
+    if (hipSetDevice(options.device_id) != hipSuccess) {
+        r.status = Status(ErrorCode::kGpuUnhealthy, "hip device not usable", kComponent);
+        return r;
+    }
+
+    auto impl = std::make_unique<Impl>();
+    Impl& I = *impl;
+    I.opt = options;
+    I.c = c;
+    I.q8 = options.quantization == HipWeightQuant::kInt8;
+    if (hipStreamCreateWithFlags(&I.stream, hipStreamNonBlocking) != hipSuccess) {
+        r.status = Status(ErrorCode::kGpuUnhealthy, "stream creation failed", kComponent);
+        return r;
+    }
+
+    const uint64_t H = c.hidden_size, qd = uint64_t(c.num_heads) * c.head_dim,
+                   kvd = uint64_t(c.num_kv_heads) * c.head_dim, In = c.intermediate_size, V = c.vocab_size;
+    size_t expected = 0;
+    std::vector<float> a, b, cbuf;
+    auto read = [&](const std::string& name, std::vector<uint64_t> shape, std::vector<float>& out) {
+        ++expected;
+        return src.Read(name, shape, out);
+    };
+#define LOAD_OR_RETURN(expr)         \
+    do {                             \
+        Status s_ = (expr);          \
+        if (!s_.ok()) {              \
+            r.status = s_;           \
+            return r;                \
+        }                            \
+    } while (0)
+
+    std::vector<float> embed;
+    LOAD_OR_RETURN(read("model.embed_tokens.weight", {V, H}, embed));
+    LOAD_OR_RETURN(UploadF32(embed, I.embed));
+    I.layers.resize(c.num_layers);
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        Impl::Layer& L = I.layers[l];
+        LOAD_OR_RETURN(read(LayerName(l, "input_layernorm.weight"), {H}, a));
+        LOAD_OR_RETURN(UploadF32(a, L.input_norm));
+        LOAD_OR_RETURN(read(LayerName(l, "post_attention_layernorm.weight"), {H}, a));
+        LOAD_OR_RETURN(UploadF32(a, L.post_norm));
+        // fused qkv: rows [q | k | v], bias concatenated the same way
+        std::vector<float> qkv, bias, t;
+        LOAD_OR_RETURN(read(LayerName(l, "self_attn.q_proj.weight"), {qd, H}, t));
+        qkv.insert(qkv.end(), t.begin(), t.end());
+        LOAD_OR_RETURN(read(LayerName(l, "self_attn.k_proj.weight"), {kvd, H}, t));
+        qkv.insert(qkv.end(), t.begin(), t.end());
+        LOAD_OR_RETURN(read(LayerName(l, "self_attn.v_proj.weight"), {kvd, H}, t));
+        qkv.insert(qkv.end(), t.begin(), t.end());
+        for (const char* nm : {"self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias"}) {
+            LOAD_OR_RETURN(read(LayerName(l, nm), {std::string(nm).find("q_proj") != std::string::npos ? qd : kvd}, t));
+            bias.insert(bias.end(), t.begin(), t.end());
+        }
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, qkv, nullptr, int64_t(qd + 2 * kvd), int64_t(H), L.qkv, I.gemv_bytes));
+        LOAD_OR_RETURN(UploadF32(bias, L.qkv_bias));
+        LOAD_OR_RETURN(read(LayerName(l, "self_attn.o_proj.weight"), {H, qd}, a));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(qd), L.o, I.gemv_bytes));
+        LOAD_OR_RETURN(read(LayerName(l, "mlp.gate_proj.weight"), {In, H}, a));
+        LOAD_OR_RETURN(read(LayerName(l, "mlp.up_proj.weight"), {In, H}, b));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, &b, int64_t(In), int64_t(H), L.gateup, I.gemv_bytes));
+        LOAD_OR_RETURN(read(LayerName(l, "mlp.down_proj.weight"), {H, In}, a));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(In), L.down, I.gemv_bytes));
+    }
+    LOAD_OR_RETURN(read("model.norm.weight", {H}, a));
+    LOAD_OR_RETURN(UploadF32(a, I.final_norm));
+    if (c.tie_word_embeddings) {
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, embed, nullptr, int64_t(V), int64_t(H), I.lm_head, I.gemv_bytes));
+    } else {
+        LOAD_OR_RETURN(read("lm_head.weight", {V, H}, a));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(V), int64_t(H), I.lm_head, I.gemv_bytes));
+    }
+    if (src.tensor_count() != expected) {
+        r.status = Status(ErrorCode::kArtifactVerificationFailed, "weight file contains unexpected tensors",
+                          kComponent);
+        return r;
+    }
+    embed.clear();
+    embed.shrink_to_fit();
+
+    // paged KV pool
+    const uint32_t bt = options.kv_block_tokens;
+    const uint64_t pool_tokens =
+        options.kv_pool_tokens ? options.kv_pool_tokens : uint64_t(std::max(1u, c.max_context_tokens)) * 4;
+    const uint32_t nblocks = uint32_t(std::max<uint64_t>(1, (pool_tokens + bt - 1) / bt));
+    I.pool.Init(nblocks, bt);
+    I.kv_layer_elems = (size_t)nblocks * c.num_kv_heads * bt * c.head_dim;
+    LOAD_OR_RETURN(I.kv.Alloc(I.kv_layer_elems * 2 * 2 * c.num_layers));
+
+    // step buffers
+    I.ldx_h = RoundUp(H, 32);
+    I.ldx_q = RoundUp(int64_t(qd), 32);
+    I.ldx_i = RoundUp(int64_t(In), 32);
+    I.qkv_n = int64_t(qd + 2 * kvd);
+    const size_t B = kMaxBatch;
+    LOAD_OR_RETURN(I.d_tokens.Alloc(B * 4));
+    LOAD_OR_RETURN(I.d_pos.Alloc(B * 4));
+    LOAD_OR_RETURN(I.d_h.Alloc(B * H * 4));
+    LOAD_OR_RETURN(I.d_xn.Alloc(B * I.ldx_h * 2));
+    LOAD_OR_RETURN(I.d_attn.Alloc(B * I.ldx_q * 2));
+    LOAD_OR_RETURN(I.d_act.Alloc(B * I.ldx_i * 2));
+    LOAD_OR_RETURN(I.d_qkv.Alloc(B * I.qkv_n * 4));
+    LOAD_OR_RETURN(I.d_q.Alloc(B * qd * 4));
+    LOAD_OR_RETURN(I.d_logits.Alloc(B * V * 4));
+    LOAD_OR_RETURN(I.d_history.Alloc(kGreedyMax * 4));
+    LOAD_OR_RETURN(I.d_step.Alloc(4));
+    LOAD_OR_RETURN(I.d_nonfinite.Alloc(B * 4));
+    // workspace: the largest need of any launch of the step (they run one
+    // after another on the stream and leave it zeroed)
+    uint64_t ws = lyk_hip_argmax_workspace_bytes(1, V);
+    for (int m = 1; m <= kMaxBatch; ++m) {
+        const Impl::Layer& L = I.layers[0];
+        const PackedMat* mats[] = {&L.qkv, &L.o, &L.down, &I.lm_head};
+        for (const PackedMat* w : mats)
+            ws = std::max(ws, lyk_hip_gemv_workspace_bytes(w->n, w->k, m, 0, 0, I.q8));
+        ws = std::max(ws, lyk_hip_gemv_workspace_bytes(L.gateup.n, L.gateup.k, m, 0, 1, I.q8));
+        ws = std::max(ws, lyk_hip_attn_workspace_bytes(m, c.num_heads, c.num_kv_heads, c.head_dim, 32));
+    }
+    I.ws_bytes = ws;
+    LOAD_OR_RETURN(I.d_ws.Alloc(ws));
+    LOAD_OR_RETURN(I.h_tokens.Alloc(B * 4));
+    LOAD_OR_RETURN(I.h_pos.Alloc(B * 4));
+    LOAD_OR_RETURN(I.h_logits.Alloc(B * V * 4));
+    LOAD_OR_RETURN(I.h_history.Alloc(kGreedyMax * 4));
+    LOAD_OR_RETURN(I.h_nonfinite.Alloc(B * 4));
+    LOAD_OR_RETURN(I.EnsureRope(std::max(1u, c.max_context_tokens)));
+    if (hipDeviceSynchronize() != hipSuccess) {
+        r.status = Status(ErrorCode::kGpuUnhealthy, "device initialisation failed", kComponent);
+        return r;
+    }
+#undef LOAD_OR_RETURN
+    model->impl_ = std::move(impl);
+    r.model = std::move(model);
+    return r;
+}
+
+QwenHipModel::~QwenHipModel() {
+    if (impl_) (void)hipSetDevice(device_id_);
+}
+
+uint32_t QwenHipModel::kv_blocks_total() const { return impl_->pool.num_blocks(); }
+uint32_t QwenHipModel::kv_blocks_free() const { return impl_->pool.free_blocks(); }
+uint64_t QwenHipModel::prefix_cache_hit_tokens() const { return impl_->prefix_hits; }
+uint64_t QwenHipModel::gemv_weight_bytes() const { return impl_->gemv_bytes; }
+
+// ---------------------------------------------------------------- sequences
+
+Status QwenHipModel::CreateSequence(uint32_t max_tokens, std::unique_ptr<SequenceState>& out) {
+    return CreateSequenceEx(max_tokens, SequenceOptions{}, out);
+}
+
+Status QwenHipModel::CreateSequenceEx(uint32_t max_tokens, const SequenceOptions& options,
+                                      std::unique_ptr<SequenceState>& out) {
+    HIP_OK(hipSetDevice(device_id_), "hip device not usable");
+    Status s = impl_->EnsureRope(std::max(1u, max_tokens));
+    if (!s.ok()) return s;
+    out = std::make_unique<HipSequenceState>(&impl_->pool, max_tokens, options);
+    return Status::Ok();
+}
+
+Status QwenHipModel::Prefill(SequenceState& state, const std::vector<uint32_t>& tokens,
+                             std::vector<float>& logits) {
+    auto& seq = static_cast<HipSequenceState&>(state);
+    if (tokens.empty()) return Status(ErrorCode::kInvalidRequest, "empty prompt", kComponent);
+    if (seq.length() != 0) return Status(ErrorCode::kInternalError, "prefill requires an empty cache", kComponent);
+    if (tokens.size() > seq.capacity())
+        return Status(ErrorCode::kContextLengthExceeded, "prompt exceeds cache capacity", kComponent);
+    for (uint32_t t : tokens)
+        if (t >= config_.vocab_size) return Status(ErrorCode::kInvalidRequest, "token id out of vocab range", kComponent);
+    HIP_OK(hipSetDevice(device_id_), "hip device not usable");
+    Impl& I = *impl_;
+    const uint32_t bt = I.pool.block_tokens();
+    const uint32_t n = uint32_t(tokens.size());
+
+    // Prefix cache: chain hashes seeded with the scope key; the block holding
+    // the last prompt token is never attached, so its logits are computed.
+    std::vector<uint64_t> hashes;
+    uint32_t start = 0;
+    if (seq.options().allow_prefix_cache) {
+        uint64_t h = 1469598103934665603ULL;
+        h = Fnv64(h, seq.options().scope_key.data(), seq.options().scope_key.size());
+        const uint32_t max_attach = (n - 1) / bt, full = n / bt;
+        std::vector<int> attached;
+        for (uint32_t b = 0; b < full; ++b) {
+            h = Fnv64(h, tokens.data() + size_t(b) * bt, bt * sizeof(uint32_t));
+            hashes.push_back(h);
+            int blk = -1;
+            if (b < max_attach && attached.size() == b && I.pool.Lookup(h, blk)) attached.push_back(blk);
+        }
+        if (!attached.empty()) {
+            start = uint32_t(attached.size()) * bt;
+            seq.AttachPrefix(std::move(attached), start);
+            I.prefix_hits += start;
+        }
+    }
+
+    std::vector<HipSequenceState*> one = {&seq};
+    for (uint32_t i = start; i < n; ++i) {
+        Status s = seq.EnsureBlocks(i);
+        if (!s.ok()) return s;
+        s = I.UploadRows(one, {tokens[i]}, {i});
+        if (!s.ok()) return s;
+        const bool last = i + 1 == n;
+        s = I.RunStep(1, Impl::SplitsFor(i + 1), last ? StepMode::kLogits : StepMode::kHidden);
+        if (!s.ok()) return s;
+        seq.Advance();
+    }
+    logits.resize(config_.vocab_size);
+    HIP_OK(hipMemcpyAsync(I.h_logits.p, I.d_logits.p, logits.size() * 4, hipMemcpyDeviceToHost, I.stream),
+           "logits download failed");
+    HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+    std::memcpy(logits.data(), I.h_logits.p, logits.size() * 4);
+
+    if (seq.options().allow_prefix_cache)
+        for (uint32_t b = 0; b < hashes.size() && b < seq.blocks().size(); ++b)
+            I.pool.Register(hashes[b], seq.blocks()[b]);
+    for (float v : logits)
+        if (!std::isfinite(v))
+            return Status(ErrorCode::kInferenceFailed, "logits contain non-finite values", kComponent);
+    return Status::Ok();
+}
+
+Status QwenHipModel::Decode(SequenceState& state, uint32_t token, std::vector<float>& logits) {
+    std::vector<DecodeBatchItem> items = {{&state, token, &logits}};
+    std::vector<Status> per_item;
+    Status s = DecodeBatch(items, per_item);
+    if (!s.ok()) return s;
+    return per_item[0];
+}
+
+Status QwenHipModel::DecodeBatch(std::vector<DecodeBatchItem>& items, std::vector<Status>& per_item) {
+    per_item.assign(items.size(), Status::Ok());
+    HIP_OK(hipSetDevice(device_id_), "hip device not usable");
+    Impl& I = *impl_;
+    std::vector<size_t> valid;
+    for (size_t i = 0; i < items.size(); ++i) {
+        auto* st = static_cast<HipSequenceState*>(items[i].state);
+        if (items[i].token >= config_.vocab_size) {
+            per_item[i] = Status(ErrorCode::kInvalidRequest, "token id out of vocab range", kComponent);
+        } else if (st->length() >= st->capacity()) {
+            per_item[i] = Status(ErrorCode::kContextLengthExceeded, "kv cache capacity exhausted", kComponent);
+        } else {
+            Status cap = st->EnsureBlocks(st->length());
+            if (!cap.ok()) per_item[i] = cap;
+            else valid.push_back(i);
+        }
+    }
+    const size_t V = config_.vocab_size;
+    for (size_t g0 = 0; g0 < valid.size(); g0 += kMaxBatch) {
+        const size_t m = std::min<size_t>(kMaxBatch, valid.size() - g0);
+        std::vector<HipSequenceState*> seqs;
+        std::vector<uint32_t> toks, pos;
+        uint32_t max_ctx = 0;
+        for (size_t i = 0; i < m; ++i) {
+            const size_t idx = valid[g0 + i];
+            auto* st = static_cast<HipSequenceState*>(items[idx].state);
+            seqs.push_back(st);
+            toks.push_back(items[idx].token);
+            pos.push_back(st->length());
+            max_ctx = std::max(max_ctx, st->length() + 1);
+        }
+        Status s = I.UploadRows(seqs, toks, pos);
+        if (!s.ok()) return s;
+        s = I.RunStep(int(m), Impl::SplitsFor(max_ctx), StepMode::kLogits);
+        if (!s.ok()) return s;
+        HIP_OK(hipMemcpyAsync(I.h_logits.p, I.d_logits.p, m * V * 4, hipMemcpyDeviceToHost, I.stream),
+               "logits download failed");
+        HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+        const float* hl = I.h_logits.as<float>();
+        for (size_t i = 0; i < m; ++i) {
+            const size_t idx = valid[g0 + i];
+            std::vector<float>& out = *items[idx].logits;
+            out.assign(hl + i * V, hl + (i + 1) * V);
+            bool finite = true;
+            for (float v : out)
+                if (!std::isfinite(v)) {
+                    finite = false;
+                    break;
+                }
+            if (!finite)
+                per_item[idx] = Status(ErrorCode::kInferenceFailed, "logits contain non-finite values", kComponent);
+            else
+                seqs[i]->Advance();
+        }
+    }
+    return Status::Ok();
+}
+
+Status QwenHipModel::GreedyRun(SequenceState& state, uint32_t token, uint32_t max_new,
+                               std::vector<uint32_t>& out_tokens) {
+    auto& seq = static_cast<HipSequenceState&>(state);
+    out_tokens.clear();
+    if (token >= config_.vocab_size)
+        return Status(ErrorCode::kInvalidRequest, "token id out of vocab range", kComponent);
+    if (max_new == 0) return Status(ErrorCode::kInvalidRequest, "max_new must be > 0", kComponent);
+    if (seq.length() >= seq.capacity())
+        return Status(ErrorCode::kContextLengthExceeded, "kv cache capacity exhausted", kComponent);
+    HIP_OK(hipSetDevice(device_id_), "hip device not usable");
+    Impl& I = *impl_;
+    const uint32_t len = seq.length();
+    const uint32_t steps = std::min({max_new, kGreedyMax, seq.capacity() - len});
+    Status s = seq.EnsureBlocks(len + steps - 1);
+    if (!s.ok()) return s;
+    s = I.UploadRows({&seq}, {token}, {len});
+    if (!s.ok()) return s;
+    HIP_OK(hipMemsetAsync(I.d_step.p, 0, 4, I.stream), "step reset failed");
+    HIP_OK(hipMemsetAsync(I.d_nonfinite.p, 0, 4, I.stream), "flag reset failed");
+    // one split count for the whole run, sized for its final context
+    const int splits = Impl::SplitsFor(len + steps);
+    for (uint32_t i = 0; i < steps; ++i) {
+        s = I.RunStep(1, splits, StepMode::kGreedy);
+        if (!s.ok()) return s;
+    }
+    HIP_OK(hipMemcpyAsync(I.h_history.p, I.d_history.p, steps * 4, hipMemcpyDeviceToHost, I.stream),
+           "token download failed");
+    HIP_OK(hipMemcpyAsync(I.h_nonfinite.p, I.d_nonfinite.p, 4, hipMemcpyDeviceToHost, I.stream),
+           "flag download failed");
+    HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+    if (I.h_nonfinite.as<int32_t>()[0] != 0)
+        return Status(ErrorCode::kInferenceFailed, "logits contain non-finite values", kComponent);
+    const int32_t* hist = I.h_history.as<int32_t>();
+    out_tokens.assign(hist, hist + steps);
+    seq.Advance(steps);
+    return Status::Ok();
+}
+
+}  // namespace lykuro::nie

@@ -1,0 +1,151 @@
+// QwenHipModel: the MI355X `hip` backend of the Lykuro engine.
+//
+// Implements the engine's GenerativeModel interface
+// (model/architectures/generative_model.h:40-105) for the
+// approved_qwen_decoder_v1 architecture, with the same factory convention,
+// error codes and ownership rules as the CUDA backend
+// (backends/cuda/qwen_cuda_model.h:42-106), so `--backend hip` can be wired
+// into the engine, CLI and servers without touching them.
+//
+// Weights are quantized at load (int4 in groups of 32 with fp16 scales, or
+// int8 per output row with fp16 scales) and repacked into the tile layouts
+// of include/lykuro_hip.h; activations between kernels are fp16, the
+// residual stream and logits fp32, the paged KV cache fp16. Every device
+// computation is one of the hand-written gfx950 kernels behind the C ABI.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "core/engine/error.h"
+#include "model/architectures/generative_model.h"
+#include "model/loader/safetensors.h"
+#include "model/manifest/manifest.h"
+
+namespace lykuro::nie {
+
+enum class HipWeightQuant {
+    kInt4,  // symmetric, groups of 32 along K, fp16 scale per group
+    kInt8,  // symmetric, one fp16 scale per output row
+};
+
+struct HipModelOptions {
+    int device_id = 0;
+    // Total KV pool capacity in tokens (0 = 4x max context) and the paged
+    // block granularity.
+    uint32_t kv_pool_tokens = 0;
+    uint32_t kv_block_tokens = 16;
+    HipWeightQuant quantization = HipWeightQuant::kInt4;
+    // Replay the decode step as a HIP graph (off: direct launches).
+    bool use_graphs = true;
+};
+
+// fp32 weights by reference tensor name. The safetensors file is one source;
+// a seeded synthetic generator is another (benchmarks without checkpoints).
+class WeightSource {
+public:
+    virtual ~WeightSource() = default;
+    // Fills `out` with the tensor as fp32, or fails when it is missing or its
+    // shape differs from `shape`.
+    virtual Status Read(const std::string& name, const std::vector<uint64_t>& shape,
+                        std::vector<float>& out) const = 0;
+    // Number of tensors the source holds (the loader rejects extras).
+    virtual size_t tensor_count() const = 0;
+};
+
+// A safetensors file as a weight source (F32 / F16 / BF16, widened to fp32
+// with the reference's codecs).
+class SafetensorsWeightSource final : public WeightSource {
+public:
+    explicit SafetensorsWeightSource(const SafetensorsFile& file) : file_(file) {}
+    Status Read(const std::string& name, const std::vector<uint64_t>& shape,
+                std::vector<float>& out) const override;
+    size_t tensor_count() const override { return file_.header().tensors.size(); }
+
+private:
+    const SafetensorsFile& file_;
+};
+
+// Seeded N(0, sigma^2) weights (norms 1.0): value i of tensor (kind, layer)
+// is element i of stream kind*1000+layer of the generator lyk_synth_normal.
+class SyntheticWeightSource final : public WeightSource {
+public:
+    SyntheticWeightSource(uint64_t seed, float sigma, size_t tensors)
+        : seed_(seed), sigma_(sigma), tensors_(tensors) {}
+    Status Read(const std::string& name, const std::vector<uint64_t>& shape,
+                std::vector<float>& out) const override;
+    size_t tensor_count() const override { return tensors_; }
+
+private:
+    uint64_t seed_;
+    float sigma_;
+    size_t tensors_;
+};
+
+// Architecture parameters, derived and validated as QwenConfig::FromManifest
+// does (model/architectures/qwen/qwen_model.cpp:88-124).
+struct HipQwenConfig {
+    uint32_t vocab_size = 0, hidden_size = 0, num_layers = 0, num_heads = 0, num_kv_heads = 0,
+             head_dim = 0, intermediate_size = 0, max_context_tokens = 0;
+    float rms_norm_eps = 1e-6f;
+    float rope_theta = 10000.0f;
+    bool tie_word_embeddings = false;
+    std::vector<uint32_t> eos_token_ids;
+
+    static Status FromManifest(const ModelManifest& manifest, HipQwenConfig& out);
+};
+
+class QwenHipModel : public GenerativeModel {
+public:
+    struct LoadResult {
+        Status status;
+        std::unique_ptr<QwenHipModel> model;
+    };
+
+    // Quantizes, repacks and uploads the verified weights to `device_id`.
+    // Fails (unsupported_model / gpu_oom / gpu_unhealthy /
+    // artifact_verification_failed) without partial residency.
+    static LoadResult Load(const ModelManifest& manifest, const SafetensorsFile& weights,
+                           const HipModelOptions& options);
+    static LoadResult Load(const ModelManifest& manifest, const WeightSource& weights,
+                           const HipModelOptions& options);
+
+    ~QwenHipModel() override;
+    QwenHipModel(const QwenHipModel&) = delete;
+    QwenHipModel& operator=(const QwenHipModel&) = delete;
+
+    const ModelLimits& limits() const override { return limits_; }
+    Status CreateSequence(uint32_t max_tokens, std::unique_ptr<SequenceState>& out) override;
+    Status CreateSequenceEx(uint32_t max_tokens, const SequenceOptions& options,
+                            std::unique_ptr<SequenceState>& out) override;
+    Status Prefill(SequenceState& state, const std::vector<uint32_t>& tokens,
+                   std::vector<float>& logits) override;
+    Status Decode(SequenceState& state, uint32_t token, std::vector<float>& logits) override;
+    Status DecodeBatch(std::vector<DecodeBatchItem>& items, std::vector<Status>& per_item) override;
+    bool SupportsGreedyRun() const override { return true; }
+    Status GreedyRun(SequenceState& state, uint32_t token, uint32_t max_new,
+                     std::vector<uint32_t>& out_tokens) override;
+
+    const HipQwenConfig& config() const { return config_; }
+
+    // Paged-KV / prefix-cache introspection (tests, capacity metrics).
+    uint32_t kv_blocks_total() const;
+    uint32_t kv_blocks_free() const;
+    uint64_t prefix_cache_hit_tokens() const;
+    // Bytes of quantized GEMV weights streamed per decode token.
+    uint64_t gemv_weight_bytes() const;
+
+    struct Impl;
+
+private:
+    QwenHipModel() = default;
+
+    HipQwenConfig config_;
+    ModelLimits limits_;
+    int device_id_ = 0;
+    std::unique_ptr<Impl> impl_;
+};
+
+}  // namespace lykuro::nie

@@ -50,6 +50,33 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Publishes this wave's earlier agent-scope (sc1) atomic stores before a
+// following arrival counter update: s_waitcnt 0 returns only once those
+// stores are performed at the device coherence point. (A workgroup-scope
+// fence does not wait for them; an agent-scope fence would also write back
+// the whole L2, which costs ~20 ns per workgroup.)
+__device__ __forceinline__ void publish_sc1_stores() {
+    __builtin_amdgcn_s_waitcnt(0);
+}
+
+// Arrival at a per-tile counter after publishing sc1 partial stores; true for
+// the last of `expected` arrivals. Call with the whole wave; lane 0 counts.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected) {
+    publish_sc1_stores();
+    unsigned prev = 0;
+    if ((threadIdx.x & 63) == 0)
+        prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0, 64);
+    return prev == expected - 1;
+}
+
+__device__ __forceinline__ void store_sc1(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_sc1(float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 }  // namespace lyk

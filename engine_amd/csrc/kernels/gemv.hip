@@ -39,7 +39,9 @@ Plan make_plan(int64_t n, int64_t k, int paired, int q8, int ksplit) {
     p.tiles = paired ? ceil_div(n, 32) : ceil_div(n, 64);
     const int64_t units = q8 ? ceil_div(k, 16) : ceil_div(k, 32);
     p.chunks = ceil_div(units, 8);
+    // default: aim for ~4096 waves, at most 16 sharing one tile's K range
     int wpt = ksplit > 0 ? ksplit : ceil_div(4096, p.tiles);
+    if (ksplit <= 0 && wpt > 16) wpt = 16;
     if (wpt > p.chunks) wpt = p.chunks;
     if (wpt < 1) wpt = 1;
     p.waves = wpt < kMaxWaves ? wpt : kMaxWaves;
@@ -116,24 +118,26 @@ __device__ __forceinline__ void finish(float (&acc)[M], int tile, int split,
         v[m] = s;
     }
     if (splits > 1) {
+        // Split-K across workgroups: partials are agent-scope (sc1) atomic
+        // stores, coherent across the XCDs' L2s; they are published before
+        // the arrival is counted, and the last arrival adds them in split
+        // order, then zeroes them and the counter.
         const size_t npad = (size_t)tiles * 64;
 #pragma unroll
         for (int m = 0; m < M; ++m)
-            partial[((size_t)split * M + m) * npad + tile * 64 + lane] = v[m];
-        __threadfence();
-        unsigned prev = 0;
-        if (lane == 0) prev = atomicAdd(&counters[tile], 1u);
-        prev = __shfl(prev, 0, 64);
-        if (prev != (unsigned)(splits - 1)) return;
-        __threadfence();
+            store_sc1(&partial[((size_t)split * M + m) * npad + tile * 64 + lane], v[m]);
+        if (!arrive_last(&counters[tile], (unsigned)splits)) return;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             float s = 0.0f;
-            for (int sp = 0; sp < splits; ++sp)
-                s += partial[((size_t)sp * M + m) * npad + tile * 64 + lane];
+            for (int sp = 0; sp < splits; ++sp) {
+                float* p = &partial[((size_t)sp * M + m) * npad + tile * 64 + lane];
+                s += load_sc1(p);
+                *p = 0.0f;  // the workspace is all zero again after every launch
+            }
             v[m] = s;
         }
-        if (lane == 0) counters[tile] = 0u;  // ready for the next launch
+        if (lane == 0) counters[tile] = 0u;
     }
     epilogue<M, EPI>(v, tile, lane, n, y, ldy, bias);
 }
@@ -457,13 +461,10 @@ int lyk_hip_gemv_splits(int64_t n, int64_t k, int m, int paired, int q8) {
     return p.splits * p.waves;
 }
 
-uint64_t lyk_hip_gemv_workspace_bytes(int64_t n, int m, int splits, int paired) {
-    // Worst case over K: one wave per chunk, every wave its own split.
-    if (n <= 0 || m < 1) return 0;
-    const int tiles = paired ? ceil_div(n, 32) : ceil_div(n, 64);
-    const int s = splits > 0 ? splits : 4096;
-    const uint64_t counters = (uint64_t(tiles) * 4 + 255) / 256 * 256;
-    return counters + uint64_t(s) * m * tiles * 64 * 4;
+uint64_t lyk_hip_gemv_workspace_bytes(int64_t n, int64_t k, int m, int splits, int paired,
+                                      int q8) {
+    if (n <= 0 || k <= 0 || m < 1) return 0;
+    return workspace_for(make_plan(n, k, paired, q8, splits), m);
 }
 
 int lyk_hip_gemv_q4(const void* d_qw, const void* d_qs, int64_t n, int64_t k,

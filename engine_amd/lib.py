@@ -10,6 +10,8 @@ import ctypes as C
 import os
 import re
 
+import torch  # noqa: F401  -- load PyTorch's HIP runtime first, so one runtime serves both
+
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 KERNEL_LIB = os.path.join(PKG, "liblykuro_hip.so")
@@ -44,10 +46,50 @@ _KERNEL_SIGS = {
     "lyk_hip_q8_unpack": (I, [P, P, I64, I64, I, P, P, P]),
     "lyk_hip_q4_dequant": (I, [P, P, I64, I64, I, P, P]),
     "lyk_hip_q8_dequant": (I, [P, P, I64, I64, I, P, P]),
-    "lyk_hip_gemv_workspace_bytes": (U64, [I64, I, I, I]),
+    "lyk_hip_gemv_workspace_bytes": (U64, [I64, I64, I, I, I, I]),
+    "lyk_hip_rmsnorm_f16": (I, [P, I64, P, F, I, I64, P, I64, P]),
+    "lyk_hip_embed_rmsnorm": (I, [P, I64, P, I, I64, P, I64, P, F, P, I64, P]),
+    "lyk_hip_rope_kv_append": (I, [P, I64, I, I, I, I, P, P, P, I, P, P, P, P, I, I, I, P]),
+    "lyk_hip_attn_workspace_bytes": (U64, [I, I, I, I, I]),
+    "lyk_hip_attn_decode": (I, [P, P, P, P, I, P, I, I, I, I, I, I, I, P, I64, P, U64, P]),
+    "lyk_hip_argmax_workspace_bytes": (U64, [I, I64]),
+    "lyk_hip_argmax": (I, [P, I64, I, I64, P, P, P, P, P, P, U64, P]),
     "lyk_hip_gemv_splits": (I, [I64, I64, I, I, I]),
     "lyk_hip_gemv_q4": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
     "lyk_hip_gemv_q8": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
+}
+
+class ModelConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "vocab_size", "hidden_size", "num_layers", "num_heads", "num_kv_heads", "head_dim",
+        "intermediate_size", "max_context_tokens")] + [
+        ("rms_norm_eps", C.c_double), ("rope_theta", C.c_double),
+        ("tie_word_embeddings", C.c_int32), ("eos_token_id", C.c_uint32)]
+
+
+class ModelOptions(C.Structure):
+    _fields_ = [("device_id", C.c_int32), ("kv_pool_tokens", C.c_uint32),
+                ("kv_block_tokens", C.c_uint32), ("quant", C.c_int32), ("use_graphs", C.c_int32)]
+
+
+I32P = C.POINTER(C.c_int32)
+_MODEL_SIGS = {
+    "lyk_model_load_safetensors": (P, [C.c_char_p, C.POINTER(ModelConfig), C.POINTER(ModelOptions), I32P]),
+    "lyk_model_load_synthetic": (P, [C.POINTER(ModelConfig), U64, F, C.POINTER(ModelOptions), I32P]),
+    "lyk_model_free": (None, [P]),
+    "lyk_model_seq_new": (P, [P, U32, C.c_int32, C.c_char_p, I32P]),
+    "lyk_model_seq_free": (None, [P]),
+    "lyk_model_seq_length": (U32, [P]),
+    "lyk_model_seq_capacity": (U32, [P]),
+    "lyk_model_prefill": (C.c_int32, [P, P, P, C.c_size_t, P]),
+    "lyk_model_decode": (C.c_int32, [P, P, U32, P]),
+    "lyk_model_decode_batch": (C.c_int32, [P, P, P, C.c_size_t, P, P]),
+    "lyk_model_greedy_run": (C.c_int32, [P, P, U32, U32, P, C.POINTER(U32)]),
+    "lyk_model_kv_blocks_total": (U32, [P]),
+    "lyk_model_kv_blocks_free": (U32, [P]),
+    "lyk_model_prefix_cache_hit_tokens": (U64, [P]),
+    "lyk_model_gemv_weight_bytes": (U64, [P]),
+    "lyk_synth_normal": (None, [U64, U64, U64, U64, F, P]),
 }
 
 _kernels = None
@@ -72,6 +114,19 @@ def kernels():
         _bind(lib, _KERNEL_SIGS)
         _kernels = lib
     return _kernels
+
+
+def model_lib():
+    """The host-model library (include/lykuro_hip_model.h)."""
+    global _model
+    if _model is None:
+        kernels()  # its dependency, from the same directory
+        if not os.path.exists(MODEL_LIB):
+            raise RuntimeError(f"{MODEL_LIB} is missing: build it with `python -m engine_amd.build`")
+        lib = C.CDLL(MODEL_LIB)
+        _bind(lib, _MODEL_SIGS)
+        _model = lib
+    return _model
 
 
 def declared_symbols(header):

@@ -1,0 +1,159 @@
+"""Python handle over QwenHipModel through include/lykuro_hip_model.h.
+
+Mirrors the engine's GenerativeModel operations (CreateSequence(Ex),
+Prefill, Decode, DecodeBatch, GreedyRun) with numpy logits; status codes are
+the engine's ErrorCode values."""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import lib as L
+
+OK, INVALID_REQUEST, UNSUPPORTED_MODEL, ARTIFACT_VERIFICATION_FAILED = 0, 1, 4, 5
+CONTEXT_LENGTH_EXCEEDED, CAPACITY_EXHAUSTED = 6, 8
+GPU_OOM, GPU_UNHEALTHY, INFERENCE_FAILED, INTERNAL_ERROR = 13, 14, 15, 17
+
+
+class ModelError(RuntimeError):
+    def __init__(self, what, code):
+        super().__init__(f"{what}: error code {code}")
+        self.code = code
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _config(cfg):
+    return L.ModelConfig(cfg.vocab_size, cfg.hidden_size, cfg.num_layers, cfg.num_heads,
+                         cfg.num_kv_heads, cfg.head_dim, cfg.intermediate_size,
+                         cfg.max_context_tokens, cfg.rms_norm_eps, cfg.rope_theta,
+                         int(cfg.tie_word_embeddings), cfg.eos_token_id)
+
+
+@dataclass
+class Options:
+    device_id: int = 0
+    kv_pool_tokens: int = 0
+    kv_block_tokens: int = 16
+    quant: str = "int4"
+    use_graphs: bool = True
+
+    def c(self):
+        return L.ModelOptions(self.device_id, self.kv_pool_tokens, self.kv_block_tokens,
+                              1 if self.quant == "int8" else 0, int(self.use_graphs))
+
+
+class HipModel:
+    def __init__(self, handle, cfg):
+        self._h = handle
+        self.cfg = cfg
+        self.vocab = cfg.vocab_size
+
+    @classmethod
+    def from_safetensors(cls, path, cfg, options: Options = Options()):
+        st = C.c_int32(0)
+        h = L.model_lib().lyk_model_load_safetensors(path.encode(), C.byref(_config(cfg)),
+                                                     C.byref(options.c()), C.byref(st))
+        if not h:
+            raise ModelError("load", st.value)
+        return cls(h, cfg)
+
+    @classmethod
+    def synthetic(cls, cfg, seed=0, sigma=0.02, options: Options = Options()):
+        st = C.c_int32(0)
+        h = L.model_lib().lyk_model_load_synthetic(C.byref(_config(cfg)), seed, sigma,
+                                                   C.byref(options.c()), C.byref(st))
+        if not h:
+            raise ModelError("load", st.value)
+        return cls(h, cfg)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            L.model_lib().lyk_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def new_seq(self, max_tokens, allow_prefix_cache=False, scope_key=""):
+        st = C.c_int32(0)
+        h = L.model_lib().lyk_model_seq_new(self._h, max_tokens, int(allow_prefix_cache),
+                                            scope_key.encode(), C.byref(st))
+        if not h:
+            raise ModelError("create sequence", st.value)
+        return Sequence(h, self)
+
+    def prefill(self, seq, tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        logits = np.zeros(self.vocab, np.float32)
+        code = L.model_lib().lyk_model_prefill(self._h, seq._h, _p(t), t.size, _p(logits))
+        return code, logits
+
+    def decode(self, seq, token):
+        logits = np.zeros(self.vocab, np.float32)
+        code = L.model_lib().lyk_model_decode(self._h, seq._h, int(token), _p(logits))
+        return code, logits
+
+    def decode_batch(self, seqs, tokens):
+        n = len(seqs)
+        handles = (C.c_void_p * n)(*[s._h for s in seqs])
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        logits = np.zeros((n, self.vocab), np.float32)
+        per = np.zeros(n, np.int32)
+        code = L.model_lib().lyk_model_decode_batch(self._h, handles, _p(t), n, _p(logits), _p(per))
+        return code, list(per), logits
+
+    def greedy_run(self, seq, token, max_new):
+        out = np.zeros(max(1, max_new), np.uint32)
+        n = C.c_uint32(0)
+        code = L.model_lib().lyk_model_greedy_run(self._h, seq._h, int(token), max_new, _p(out),
+                                                  C.byref(n))
+        return code, [int(v) for v in out[:n.value]]
+
+    @property
+    def kv_blocks_total(self):
+        return L.model_lib().lyk_model_kv_blocks_total(self._h)
+
+    @property
+    def kv_blocks_free(self):
+        return L.model_lib().lyk_model_kv_blocks_free(self._h)
+
+    @property
+    def prefix_cache_hit_tokens(self):
+        return L.model_lib().lyk_model_prefix_cache_hit_tokens(self._h)
+
+    @property
+    def gemv_weight_bytes(self):
+        return L.model_lib().lyk_model_gemv_weight_bytes(self._h)
+
+
+class Sequence:
+    def __init__(self, handle, model):
+        self._h = handle
+        self._model = model  # keep the model alive while the sequence lives
+
+    def close(self):
+        if getattr(self, "_h", None):
+            L.model_lib().lyk_model_seq_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def length(self):
+        return L.model_lib().lyk_model_seq_length(self._h)
+
+    @property
+    def capacity(self):
+        return L.model_lib().lyk_model_seq_capacity(self._h)
+
+
+def synth_normal(seed, stream, count, sigma, first=0):
+    out = np.empty(count, np.float32)
+    L.model_lib().lyk_synth_normal(seed, stream, first, count, sigma, _p(out))
+    return out

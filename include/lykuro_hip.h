@@ -15,7 +15,9 @@
  *   - Every function returns 0 (LYK_OK) or a LYK_ERR_* code; nothing throws.
  *   - No entry point allocates device memory; scratch comes from the caller's
  *     workspace, sized by the matching *_workspace_bytes function and zeroed
- *     by the caller once, before first use (kernels leave it zeroed again).
+ *     by the caller once, before first use. Every kernel returns the part it
+ *     used to zero before it exits, so one workspace can serve every call on
+ *     a stream; calls that overlap in time need separate workspaces.
  *   - fp16 values are passed as uint16_t bit patterns (IEEE binary16).
  *   - Results are deterministic: fixed-order reductions, no float atomics.
  */
@@ -118,18 +120,19 @@ int lyk_hip_q8_dequant(const void* d_qw, const void* d_qs, int64_t n,
  *     LYK_EPI_STORE_F16 y fp16 [M][ldy]: y = fp16(Wx (+ bias))
  *     LYK_EPI_SILU_F16  paired packing; y fp16 [M][ldy]:
  *                       y = fp16(silu(A x) * (B x)), silu(g) = g/(1+exp(-g))
- *   splits: 0 = choose; else the number of workgroups sharing one row tile's
- *           K range (partials merged in fixed order by the last one).
- *   workspace: lyk_hip_gemv_workspace_bytes(n, M, splits, paired) bytes,
- *              zeroed once before first use. */
+ *   splits: 0 = choose; else the number of waves sharing one row tile's K
+ *           range (at most 4 per workgroup; beyond that several workgroups,
+ *           whose partials the last to finish adds in a fixed order).
+ *   workspace: lyk_hip_gemv_workspace_bytes(n, k, M, splits, paired, q8)
+ *              bytes (0 when no split crosses workgroups). */
 enum {
     LYK_EPI_STORE = 0,
     LYK_EPI_ADD = 1,
     LYK_EPI_STORE_F16 = 2,
     LYK_EPI_SILU_F16 = 3,
 };
-uint64_t lyk_hip_gemv_workspace_bytes(int64_t n, int m, int splits,
-                                      int paired);
+uint64_t lyk_hip_gemv_workspace_bytes(int64_t n, int64_t k, int m, int splits,
+                                      int paired, int q8);
 int lyk_hip_gemv_splits(int64_t n, int64_t k, int m, int paired, int q8);
 int lyk_hip_gemv_q4(const void* d_qw, const void* d_qs, int64_t n, int64_t k,
                     const uint16_t* d_x, int64_t ldx, int m, int epilogue,
@@ -139,6 +142,69 @@ int lyk_hip_gemv_q8(const void* d_qw, const void* d_qs, int64_t n, int64_t k,
                     const uint16_t* d_x, int64_t ldx, int m, int epilogue,
                     void* d_y, int64_t ldy, const float* d_bias, int splits,
                     void* d_workspace, uint64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- decode
+ * Paged KV cache: per layer, K and V pools of fp16 [num_blocks][nkv][bt][hd]
+ * (bt = block_tokens). Token t of batch row m lives in block
+ * table[m*table_stride + t/bt], slot t%bt. Positions d_pos[m] are the
+ * 0-based position of each row's current token; its context is pos+1. */
+
+/* xn[m] = fp16(h[m] * (1/sqrt(mean(h[m]^2) + eps)) * gamma): RMSNorm
+ * (qwen_model.cpp:33-39; NormScaleKernel / RmsNormRowsKernel,
+ * qwen_cuda_model.cu:182-201, 591-610, 921-944), output ready for a GEMV. */
+int lyk_hip_rmsnorm_f16(const float* d_h, int64_t ldh, const float* d_gamma,
+                        float eps, int m, int64_t n, uint16_t* d_xn, int64_t ldx,
+                        void* stream);
+
+/* h[m] = table[tokens[m]] (fp32 rows) and xn[m] = RMSNorm(h[m]) as above
+ * (qwen_model.cpp:220-221, 235-236; GatherEmbedRowsKernel,
+ * qwen_cuda_model.cu:910-919). */
+int lyk_hip_embed_rmsnorm(const float* d_table, int64_t vocab,
+                          const int32_t* d_tokens, int m, int64_t n, float* d_h,
+                          int64_t ldh, const float* d_gamma, float eps,
+                          uint16_t* d_xn, int64_t ldx, void* stream);
+
+/* Rotate-half RoPE on the q and k parts of qkv fp32 [m][ldq] ([q | k | v],
+ * nq and nkv heads of hd), q written to d_q fp32 [m][nq*hd], rotated k and v
+ * appended to the paged caches as fp16 at each row's position. cos/sin are
+ * fp32 [max_pos][hd/2] tables of cos(p*theta^(-2i/hd)) as the CPU computes
+ * them (qwen_model.cpp:41-54, 239-253; RopeQkKernel + ScatterKv2Kernel,
+ * qwen_cuda_model.cu:822-870). Rows whose position or block is out of range
+ * are skipped. */
+int lyk_hip_rope_kv_append(const float* d_qkv, int64_t ldq, int m, int nq,
+                           int nkv, int hd, const int32_t* d_pos,
+                           const float* d_cos, const float* d_sin, int max_pos,
+                           float* d_q, uint16_t* d_kcache, uint16_t* d_vcache,
+                           const int32_t* d_table, int table_stride,
+                           int block_tokens, int num_blocks, void* stream);
+
+/* GQA decode attention of each row's query (d_q fp32 [m][nq*hd]) over its
+ * pos+1 cached tokens: out fp16 [m][ldo] = softmax(q k^T / sqrt(hd)) v per
+ * head, kv head = head / (nq/nkv) (qwen_model.cpp:255-287;
+ * BatchSplitAttentionKernel + BatchCombineAttentionKernel,
+ * qwen_cuda_model.cu:401-527). Each kv head's context is cut into `splits`
+ * ranges handled by separate workgroups and merged in split order. */
+uint64_t lyk_hip_attn_workspace_bytes(int m, int nq, int nkv, int hd,
+                                      int splits);
+int lyk_hip_attn_decode(const float* d_q, const uint16_t* d_kcache,
+                        const uint16_t* d_vcache, const int32_t* d_table,
+                        int table_stride, const int32_t* d_pos, int m, int nq,
+                        int nkv, int hd, int block_tokens, int num_blocks,
+                        int splits, uint16_t* d_out, int64_t ldo,
+                        void* d_workspace, uint64_t workspace_bytes,
+                        void* stream);
+
+/* Greedy token per row: the first index of the maximum logit, NaN never
+ * winning (Sampler's greedy rule, sampler.cpp:48-53; ArgmaxStage1/2Kernel,
+ * qwen_cuda_model.cu:1388-1458). Writes d_tokens[m]; optionally adds the
+ * row's count of non-finite logits to d_nonfinite[m], adds 1 to
+ * d_advance[m], and (m == 1 only) appends the token to d_history[*d_step]
+ * and increments *d_step -- the on-device chaining of GreedyRun. */
+uint64_t lyk_hip_argmax_workspace_bytes(int m, int64_t n);
+int lyk_hip_argmax(const float* d_logits, int64_t ldl, int m, int64_t n,
+                   int32_t* d_tokens, int32_t* d_nonfinite, int32_t* d_advance,
+                   int32_t* d_history, int32_t* d_step, void* d_workspace,
+                   uint64_t workspace_bytes, void* stream);
 
 int lyk_abi_version(void);
 

@@ -1,0 +1,258 @@
+"""QwenHipModel against the CPU oracle, through the model C ABI.
+
+The case list follows the reference's backend parity suite
+(tests/cuda/cuda_parity_test.cpp:85-558): prefill / long-prompt / decode
+trajectory parity, run-to-run determinism, capacity and vocab errors, batched
+vs sequential decode, per-item error isolation, paged-pool exhaustion, the
+prefix cache, quantized-vs-fp32 closeness, plus GreedyRun == sequential
+Decode + argmax (tests/metal/metal_fast_parity_test.cpp:123-163).
+
+Bars: greedy tokens equal the oracle's for 32 decode
+steps; logits within the stated norm-relative tolerance of the fp32 oracle on
+the dequantized weights; bit-identical repeats."""
+import numpy as np
+import pytest
+
+from engine_amd import model as M
+from oracle import oracle as O
+from tests.model_pairs import rel_err, synthetic_pair, tiny_pair, top2_gap
+
+pytestmark = pytest.mark.gpu
+
+# End-to-end logits tolerance (norm-relative) against the fp32 oracle: the
+# backend rounds GEMV inputs and K/V to fp16, ~2^-12 relative per element.
+E2E_TOL = 5e-3
+MODES = ["int4", "int8"]
+
+
+@pytest.fixture(scope="module", params=MODES)
+def tiny(request):
+    src, ref, hip = tiny_pair(request.param)
+    yield request.param, src, ref, hip
+    hip.close()
+
+
+def test_prefill_logits_match_oracle(tiny):
+    mode, _, ref, hip = tiny
+    prompt = [1, 5, 9, 2, 17, 250]
+    s, rs = hip.new_seq(128), ref.new_seq(128)
+    c1, a = hip.prefill(s, prompt)
+    c2, b = ref.prefill(rs, prompt)
+    assert c1 == c2 == 0
+    assert rel_err(a, b) < E2E_TOL
+    assert np.argmax(a) == np.argmax(b)
+
+
+def test_long_prompt_prefill_matches_oracle(tiny):
+    """cuda_parity_test.cpp:99-110 (60-token prompt)."""
+    mode, _, ref, hip = tiny
+    prompt = [1 + i * 5 % 300 for i in range(60)]
+    s, rs = hip.new_seq(128), ref.new_seq(128)
+    c1, a = hip.prefill(s, prompt)
+    c2, b = ref.prefill(rs, prompt)
+    assert c1 == c2 == 0 and rel_err(a, b) < E2E_TOL
+
+
+def test_decode_trajectory_matches_oracle(tiny):
+    """32 greedy steps, each side sampling its own logits."""
+    mode, _, ref, hip = tiny
+    s, rs = hip.new_seq(128), ref.new_seq(128)
+    _, a = hip.prefill(s, [3, 7, 11])
+    _, b = ref.prefill(rs, [3, 7, 11])
+    for step in range(32):
+        assert rel_err(a, b) < E2E_TOL, step
+        ta, tb = O.argmax(a), O.argmax(b)
+        assert ta == tb, f"greedy divergence at step {step} (oracle top-2 gap {top2_gap(b):.2e})"
+        c1, a = hip.decode(s, ta)
+        c2, b = ref.decode(rs, tb)
+        assert c1 == c2 == 0
+
+
+def test_output_is_deterministic_across_runs(tiny):
+    mode, _, _, hip = tiny
+
+    def run():
+        s = hip.new_seq(128)
+        _, logits = hip.prefill(s, [1, 2, 3])
+        for i in range(10):
+            c, logits = hip.decode(s, i * 7 % 300)
+            assert c == 0
+        return logits
+
+    a, b = run(), run()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_rejects_capacity_overrun_and_bad_tokens(tiny):
+    mode, _, _, hip = tiny
+    s = hip.new_seq(4)
+    assert hip.prefill(s, [1] * 5)[0] == M.CONTEXT_LENGTH_EXCEEDED
+    assert hip.prefill(s, [9999])[0] == M.INVALID_REQUEST
+    assert hip.prefill(s, [])[0] == M.INVALID_REQUEST
+    assert hip.prefill(s, [1, 2, 3, 4])[0] == M.OK
+    assert hip.prefill(s, [1])[0] == M.INTERNAL_ERROR
+    assert hip.decode(s, 1)[0] == M.CONTEXT_LENGTH_EXCEEDED
+    assert hip.decode(hip.new_seq(8), 303)[0] == M.INVALID_REQUEST
+
+
+def test_batched_decode_matches_sequential(tiny):
+    """cuda_parity_test.cpp:206-256, with a stronger bar: the GEMV and
+    attention arithmetic of a row does not depend on the batch, so batched
+    logits equal sequential ones bit for bit."""
+    mode, _, _, hip = tiny
+    prompts = [[1, 5, 9], [17, 4, 22, 8, 30], [7, 7, 25], [300, 2]]
+    seq = [hip.new_seq(64) for _ in prompts]
+    bat = [hip.new_seq(64) for _ in prompts]
+    sl = [hip.prefill(s, p)[1] for s, p in zip(seq, prompts)]
+    bl = [hip.prefill(s, p)[1] for s, p in zip(bat, prompts)]
+    for step in range(12):
+        toks = [O.argmax(l) for l in sl]
+        assert toks == [O.argmax(l) for l in bl]
+        for i in range(len(prompts)):
+            assert np.array_equal(sl[i].view(np.uint32), bl[i].view(np.uint32)), (step, i)
+        sl = [hip.decode(s, t)[1] for s, t in zip(seq, toks)]
+        code, per, logits = hip.decode_batch(bat, toks)
+        assert code == 0 and per == [0] * len(prompts)
+        bl = list(logits)
+
+
+def test_batched_decode_isolates_invalid_items(tiny):
+    """cuda_parity_test.cpp:258-276."""
+    mode, _, _, hip = tiny
+    good, full = hip.new_seq(64), hip.new_seq(3)
+    assert hip.prefill(good, [1, 2])[0] == 0
+    assert hip.prefill(full, [1, 2, 3])[0] == 0
+    code, per, _ = hip.decode_batch([good, full, good], [5, 6, 99999])
+    assert code == 0
+    assert per == [0, M.CONTEXT_LENGTH_EXCEEDED, M.INVALID_REQUEST]
+    assert good.length == 3 and full.length == 3
+
+
+def test_greedy_run_equals_sequential_decode(tiny):
+    """GreedyRun (on-device argmax chaining) == Decode + host argmax, bit for
+    bit (metal_fast_parity_test.cpp:123-163)."""
+    mode, _, _, hip = tiny
+    a, b = hip.new_seq(128), hip.new_seq(128)
+    _, la = hip.prefill(a, [4, 9, 16])
+    hip.prefill(b, [4, 9, 16])
+    first = O.argmax(la)
+    code, run = hip.greedy_run(b, first, 40)
+    assert code == 0 and len(run) == 40 and b.length == 43
+    seqt, t = [], first
+    for _ in range(40):
+        _, l = hip.decode(a, t)
+        t = O.argmax(l)
+        seqt.append(t)
+    assert run == seqt
+    # state continues identically afterwards
+    assert np.array_equal(hip.decode(a, 5)[1].view(np.uint32), hip.decode(b, 5)[1].view(np.uint32))
+
+
+def test_greedy_run_argument_errors(tiny):
+    mode, _, _, hip = tiny
+    s = hip.new_seq(8)
+    hip.prefill(s, [1, 2, 3])
+    assert hip.greedy_run(s, 303, 4)[0] == M.INVALID_REQUEST
+    assert hip.greedy_run(s, 1, 0)[0] == M.INVALID_REQUEST
+    code, toks = hip.greedy_run(s, 1, 100)      # capped by capacity
+    assert code == 0 and len(toks) == 5 and s.length == 8
+    assert hip.greedy_run(s, 1, 1)[0] == M.CONTEXT_LENGTH_EXCEEDED
+
+
+def test_quantized_close_to_fp32_model(tiny):
+    """cuda_parity_test.cpp:424-453: quantization error bound against the
+    unquantized model (0.05 int8, 0.4 int4 max-abs on logits)."""
+    mode, src, _, hip = tiny
+    prompt = [1, 5, 9, 2, 17, 250]
+    _, a = hip.prefill(hip.new_seq(128), prompt)
+    _, b = src.prefill(src.new_seq(128), prompt)
+    tol = 0.05 if mode == "int8" else 0.4
+    assert np.abs(a - b).max() <= tol
+
+
+# ------------------------------------------------------- paged pool / prefix
+def _pool_model(mode, pool_tokens):
+    _, _, hip = tiny_pair(mode, options=M.Options(quant=mode, kv_pool_tokens=pool_tokens,
+                                                  kv_block_tokens=16))
+    return hip
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_paged_pool_exhaustion_reports_capacity(cuda, mode):
+    """cuda_parity_test.cpp:280-305."""
+    hip = _pool_model(mode, 32)  # 2 blocks of 16
+    s = hip.new_seq(128)
+    assert hip.prefill(s, [1] * 40)[0] == M.CAPACITY_EXHAUSTED
+    s.close()
+    assert hip.kv_blocks_free == hip.kv_blocks_total == 2
+    hip.close()
+
+
+def test_prefix_cache_reuses_blocks_within_scope(cuda):
+    """cuda_parity_test.cpp:307-367."""
+    hip = _pool_model("int4", 512)
+    prompt = [1 + i % 250 for i in range(40)]
+    first = hip.new_seq(128, True, "tn_a/prj_1")
+    _, l1 = hip.prefill(first, prompt)
+    assert hip.prefix_cache_hit_tokens == 0
+    second = hip.new_seq(128, True, "tn_a/prj_1")
+    _, l2 = hip.prefill(second, prompt)
+    assert hip.prefix_cache_hit_tokens == 32
+    assert np.array_equal(l1, l2)
+    pristine = l1.copy()
+    for _ in range(8):
+        t1, t2 = O.argmax(l1), O.argmax(l2)
+        assert t1 == t2
+        _, l1 = hip.decode(first, t1)
+        _, l2 = hip.decode(second, t2)
+    third = hip.new_seq(128, True, "tn_b/prj_9")
+    _, l3 = hip.prefill(third, prompt)
+    assert hip.prefix_cache_hit_tokens == 32
+    assert np.array_equal(pristine, l3)
+    hip.close()
+
+
+def test_prefix_cache_disabled_by_default(cuda):
+    hip = _pool_model("int4", 512)
+    for _ in range(2):
+        s = hip.new_seq(128)
+        assert hip.prefill(s, [7] * 40)[0] == 0
+    assert hip.prefix_cache_hit_tokens == 0
+    hip.close()
+
+
+def test_prefix_cache_eviction_reclaims_unreferenced_blocks(cuda):
+    """cuda_parity_test.cpp:388-420."""
+    hip = _pool_model("int4", 64)  # 4 blocks
+    a = hip.new_seq(128, True, "tn_a")
+    assert hip.prefill(a, [3] * 40)[0] == 0
+    a.close()
+    assert hip.kv_blocks_free == hip.kv_blocks_total
+    b = hip.new_seq(128, True, "tn_a")
+    assert hip.prefill(b, [9] * 48)[0] == 0
+    b.close()
+    hip.close()
+
+
+# ---------------------------------------------------- synthetic, larger
+MID = O.QwenConfig(2048, 512, 3, 8, 2, 64, 1408, 512, 1e-6, 1e6, False, 2047)
+MID128 = O.QwenConfig(4096, 1024, 2, 8, 2, 128, 2816, 512, 1e-6, 1e6, True, 4095)
+
+
+@pytest.mark.parametrize("cfg", [MID, MID128], ids=["hd64", "hd128"])
+@pytest.mark.parametrize("mode", MODES)
+def test_synthetic_model_greedy_32_steps(cuda, cfg, mode):
+    src, ref, hip = synthetic_pair(cfg, mode, seed=3)
+    prompt = list(O.synth_tokens(1, 0, 24, cfg.vocab_size))
+    s, rs = hip.new_seq(cfg.max_context_tokens), ref.new_seq(cfg.max_context_tokens)
+    _, a = hip.prefill(s, prompt)
+    _, b = ref.prefill(rs, prompt)
+    errs = []
+    for step in range(32):
+        errs.append(rel_err(a, b))
+        ta, tb = O.argmax(a), O.argmax(b)
+        assert ta == tb, f"step {step}: {ta} != {tb}, oracle top-2 gap {top2_gap(b):.3e}"
+        _, a = hip.decode(s, ta)
+        _, b = ref.decode(rs, tb)
+    assert max(errs) < E2E_TOL, errs
+    hip.close()
