@@ -214,10 +214,12 @@ private:
     uint64_t tick_ = 0;
 };
 
+// Holds a reference to the pool, so destroying a sequence after its model is
+// still safe; blocks go back to the pool on destruction.
 class HipSequenceState final : public SequenceState {
 public:
-    HipSequenceState(KvPool* pool, uint32_t max_tokens, SequenceOptions options)
-        : pool_(pool), max_tokens_(max_tokens), options_(std::move(options)) {}
+    HipSequenceState(std::shared_ptr<KvPool> pool, uint32_t max_tokens, SequenceOptions options)
+        : pool_(std::move(pool)), max_tokens_(max_tokens), options_(std::move(options)) {}
     ~HipSequenceState() override {
         for (int b : blocks_) pool_->Release(b);
     }
@@ -244,7 +246,7 @@ public:
     void Advance(uint32_t n = 1) { length_ += n; }
 
 private:
-    KvPool* pool_;
+    std::shared_ptr<KvPool> pool_;
     uint32_t max_tokens_;
     uint32_t length_ = 0;
     SequenceOptions options_;
@@ -378,7 +380,8 @@ struct QwenHipModel::Impl {
     PackedMat lm_head;
     std::vector<Layer> layers;
 
-    KvPool pool;
+    std::shared_ptr<KvPool> pool_ref = std::make_shared<KvPool>();
+    KvPool& pool = *pool_ref;
     DevBuf kv;  // [layer][K|V][num_blocks][nkv][bt][hd] fp16
     size_t kv_layer_elems = 0;
 
@@ -388,8 +391,9 @@ struct QwenHipModel::Impl {
     // decode-step buffers (kMaxBatch rows)
     int64_t ldx_h = 0, ldx_q = 0, ldx_i = 0, qkv_n = 0;
     DevBuf d_tokens, d_pos, d_tables, d_h, d_xn, d_attn, d_act, d_qkv, d_q, d_logits, d_ws,
-        d_history, d_step, d_nonfinite;
-    PinnedBuf h_tokens, h_pos, h_tables, h_logits, h_history, h_nonfinite;
+        d_history, d_step, d_nonfinite, d_prompt;
+    PinnedBuf h_tokens, h_pos, h_tables, h_logits, h_history, h_nonfinite, h_prompt;
+    size_t prompt_cap = 0;
     uint64_t ws_bytes = 0;
 
     std::map<uint64_t, hipGraphExec_t> graphs;
@@ -782,7 +786,7 @@ Status QwenHipModel::CreateSequenceEx(uint32_t max_tokens, const SequenceOptions
     HIP_OK(hipSetDevice(device_id_), "hip device not usable");
     Status s = impl_->EnsureRope(std::max(1u, max_tokens));
     if (!s.ok()) return s;
-    out = std::make_unique<HipSequenceState>(&impl_->pool, max_tokens, options);
+    out = std::make_unique<HipSequenceState>(impl_->pool_ref, max_tokens, options);
     return Status::Ok();
 }
 
@@ -822,16 +826,41 @@ Status QwenHipModel::Prefill(SequenceState& state, const std::vector<uint32_t>& 
         }
     }
 
-    std::vector<HipSequenceState*> one = {&seq};
-    for (uint32_t i = start; i < n; ++i) {
-        Status s = seq.EnsureBlocks(i);
+    if (start < n) {
+        Status s = seq.EnsureBlocks(n - 1);
         if (!s.ok()) return s;
-        s = I.UploadRows(one, {tokens[i]}, {i});
+        // Tokens and positions of the whole prompt go up in one copy; each
+        // step then takes its row with a device-to-device copy, so no host
+        // staging buffer is rewritten while a copy from it may be pending.
+        const size_t rows = n - start;
+        if (rows * 2 > I.prompt_cap) {
+            HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+            I.prompt_cap = std::max<size_t>(rows * 2, 1024);
+            s = I.d_prompt.Alloc(I.prompt_cap * 4);
+            if (!s.ok()) return s;
+            s = I.h_prompt.Alloc(I.prompt_cap * 4);
+            if (!s.ok()) return s;
+        }
+        int32_t* hp = I.h_prompt.as<int32_t>();
+        for (size_t r = 0; r < rows; ++r) {
+            hp[2 * r] = int32_t(tokens[start + r]);
+            hp[2 * r + 1] = int32_t(start + r);
+        }
+        HIP_OK(hipMemcpyAsync(I.d_prompt.p, hp, rows * 8, hipMemcpyHostToDevice, I.stream),
+               "prompt upload failed");
+        s = I.UploadRows({&seq}, {tokens[start]}, {start});
         if (!s.ok()) return s;
-        const bool last = i + 1 == n;
-        s = I.RunStep(1, Impl::SplitsFor(i + 1), last ? StepMode::kLogits : StepMode::kHidden);
-        if (!s.ok()) return s;
-        seq.Advance();
+        for (uint32_t i = start; i < n; ++i) {
+            const int32_t* row = I.d_prompt.as<int32_t>() + 2 * size_t(i - start);
+            HIP_OK(hipMemcpyAsync(I.d_tokens.p, row, 4, hipMemcpyDeviceToDevice, I.stream),
+                   "token copy failed");
+            HIP_OK(hipMemcpyAsync(I.d_pos.p, row + 1, 4, hipMemcpyDeviceToDevice, I.stream),
+                   "position copy failed");
+            const bool last = i + 1 == n;
+            s = I.RunStep(1, Impl::SplitsFor(i + 1), last ? StepMode::kLogits : StepMode::kHidden);
+            if (!s.ok()) return s;
+        }
+        seq.Advance(n - start);
     }
     logits.resize(config_.vocab_size);
     HIP_OK(hipMemcpyAsync(I.h_logits.p, I.d_logits.p, logits.size() * 4, hipMemcpyDeviceToHost, I.stream),

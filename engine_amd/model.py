@@ -6,6 +6,7 @@ the engine's ErrorCode values."""
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -52,6 +53,7 @@ class HipModel:
         self._h = handle
         self.cfg = cfg
         self.vocab = cfg.vocab_size
+        self._seqs = weakref.WeakSet()
 
     @classmethod
     def from_safetensors(cls, path, cfg, options: Options = Options()):
@@ -72,7 +74,10 @@ class HipModel:
         return cls(h, cfg)
 
     def close(self):
+        """Frees the model; sequences still open are freed first."""
         if getattr(self, "_h", None):
+            for s in list(self._seqs):
+                s.close()
             L.model_lib().lyk_model_free(self._h)
             self._h = None
 
@@ -85,7 +90,9 @@ class HipModel:
                                             scope_key.encode(), C.byref(st))
         if not h:
             raise ModelError("create sequence", st.value)
-        return Sequence(h, self)
+        seq = Sequence(h, self)
+        self._seqs.add(seq)
+        return seq
 
     def prefill(self, seq, tokens):
         t = np.ascontiguousarray(tokens, dtype=np.uint32)

@@ -143,7 +143,7 @@ def test_rope_kv_append_bit_exact(cuda, nq, nkv, hd):
     rng = np.random.default_rng(hd)
     m, bt, cap, theta = 3, 16, 300, 1e6
     pos = np.array([0, 17, 299], np.int32)
-    nblocks = 40
+    nblocks = 64
     table = rng.permutation(nblocks)[: m * 19].reshape(m, 19).astype(np.int32)
     qkv = rng.standard_normal((m, (nq + 2 * nkv) * hd)).astype(np.float32)
     cs, sn = rope_tables(cap, hd, theta)
