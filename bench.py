@@ -1,0 +1,250 @@
+"""Decode throughput of the hip backend: Qwen2.5-7B-architecture INT4
+weight-only decode at batch 1 on one MI355X (BASELINE.json metric, config 4).
+
+  python bench.py [--steps K] [--warmup W] [--prompt P] [--quant int4|int8]
+
+A step is one decode token of one sequence (GreedyRun: the whole forward plus
+on-device argmax, replayed as a HIP graph). Weights are random-init
+N(0, 0.02) (synthetic, no checkpoint) quantized at load; the prompt is
+2048 uniform random token ids. One JSON line is printed:
+  value        decode tokens/s (whole job; one GPU)
+  roofline     the dominant kernel (the fused gate/up INT4 GEMV at 7B shape),
+               algorithmic bytes per launch / average launch time from HIP
+               events, weights rotated over > 2x the 256 MB MALL
+  cpu_baseline the reference engine's own CPU QwenModel (oracle/_ref), single
+               thread as the reference runs it, on a bounded sample (see
+               cpu_baseline.sample); the C restatement (oracle) if _ref is absent
+Only N=1 is supported: this build targets one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
+
+
+def qwen7b(max_context=32768):
+    from oracle.oracle import QwenConfig
+    return QwenConfig(152064, 3584, 28, 28, 4, 128, 18944, max_context, 1e-6, 1e6, False, 151643)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ decode
+def run_decode(args):
+    import torch
+    from engine_amd import model as M
+
+    cfg = qwen7b()
+    t0 = time.time()
+    opts = M.Options(quant=args.quant, kv_pool_tokens=args.prompt + args.warmup + args.steps + 512)
+    hip = M.HipModel.synthetic(cfg, seed=0, sigma=0.02, options=opts)
+    log(f"[bench] load (synthetic 7B, {args.quant}) {time.time() - t0:.1f}s, "
+        f"GEMV bytes/token {hip.gemv_weight_bytes / 1e9:.3f} GB")
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, cfg.vocab_size, args.prompt).astype(np.uint32)
+    seq = hip.new_seq(args.prompt + args.warmup + args.steps + 8)
+    t0 = time.time()
+    code, logits = hip.prefill(seq, prompt)
+    assert code == 0, f"prefill failed with code {code}"
+    log(f"[bench] prefill {args.prompt} tokens {time.time() - t0:.1f}s")
+    tok = int(np.argmax(logits))
+
+    def greedy(n, tok):
+        out = []
+        while len(out) < n:
+            code, toks = hip.greedy_run(seq, tok, min(256, n - len(out)))
+            assert code == 0 and toks, f"greedy run failed with code {code}"
+            out += toks
+            tok = toks[-1]
+        return out, tok
+
+    if args.warmup:
+        _, tok = greedy(args.warmup, tok)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks, tok = greedy(args.steps, tok)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ctx = seq.length
+    # algorithmic bytes of one timed step: the packed GEMV weights + scales,
+    # plus K and V (fp16) of the mean context over the timed steps
+    kv_per_ctx = cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
+    step_bytes = hip.gemv_weight_bytes + kv_per_ctx * (ctx - args.steps / 2)
+    gemv_bytes = hip.gemv_weight_bytes
+    hip.close()
+    return dict(tok_s=args.steps / dt, ms=dt * 1e3 / args.steps, ctx_end=ctx,
+                step_bytes=step_bytes, gemv_bytes=gemv_bytes, tokens=toks)
+
+
+# -------------------------------------------------------- dominant kernel
+def gemv_roofline(quant, reps=200):
+    """Fused gate/up GEMV (Qwen2.5-7B: 2 x [18944, 3584], M=1) timed with HIP
+    events on its launch stream, over weight copies > 2x the MALL."""
+    import torch
+    import engine_amd.lib as L
+    from engine_amd import ops
+
+    n, k = 18944, 3584
+    rng = np.random.default_rng(1)
+    g = (rng.standard_normal((n, k), dtype=np.float32) * 0.02)
+    u = (rng.standard_normal((n, k), dtype=np.float32) * 0.02)
+    pw0 = ops.PackedWeight.from_float(quant, g, u)
+    qw, qs = pw0.qw.cpu().numpy(), pw0.qs.cpu().numpy()
+    copies = max(2, int(np.ceil(640e6 / pw0.nbytes)))
+    pws = [pw0] + [ops.PackedWeight(quant, n, k, qw, qs, True) for _ in range(copies - 1)]
+    x = torch.randn(1, k, device="cuda").half()
+    y = torch.empty((1, n), dtype=torch.float16, device="cuda")
+    ws = ops.Workspace(64 << 20)
+    st = torch.cuda.Stream()
+    fn = L.kernels().lyk_hip_gemv_q4 if quant == "int4" else L.kernels().lyk_hip_gemv_q8
+    sp = ops.stream_ptr(st)
+    argv = [(ops._p(p.qw), ops._p(p.qs), n, k, ops._p(x), k, 1, L.EPI_SILU_F16, ops._p(y), n, None, 0,
+             ops._p(ws.buf), ws.nbytes, sp) for p in pws]
+    for a in argv[:4]:
+        assert fn(*a) == 0
+    st.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(reps):
+        fn(*argv[i % copies])
+    e1.record(st)
+    st.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    alg = pw0.nbytes + k * 2 + n * 2
+    achieved = alg / us / 1e3
+    return dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None,
+                kernel=f"gemv_{quant} gate/up paired 2x[{n},{k}] M=1", avg_us=round(us, 2),
+                bytes_per_launch=alg)
+
+
+# ----------------------------------------------------------- CPU baseline
+def cpu_baseline(tokens=3):
+    """Reference QwenModel (oracle/_ref) on the 7B architecture, single thread,
+    with 1 and then 2 decoder layers; per-token time extrapolated to 28
+    layers as t(1) + 27 * (t(2) - t(1)). Weights are random fp16 in a
+    safetensors file (values do not change CPU time); the head is tied to the
+    embedding, the same [152064, 3584] matvec as the untied 7B head."""
+    from oracle import oracle as O
+    import dataclasses
+
+    use_ref = O.ref_available()
+    base = dataclasses.replace(qwen7b(64), tie_word_embeddings=True)
+    rng = np.random.default_rng(2)
+    block = (rng.standard_normal(1 << 24).astype(np.float32) * 0.02)
+    times = {}
+    for layers in (1, 2):
+        cfg = dataclasses.replace(base, num_layers=layers)
+        if use_ref:
+            tensors = {}
+            names = [("model.embed_tokens.weight", cfg.shape(O.T_EMBED)),
+                     ("model.norm.weight", cfg.shape(O.T_FINAL_NORM))]
+            for l in range(layers):
+                for kind, suffix in O.LAYER_NAMES.items():
+                    names.append((f"model.layers.{l}.{suffix}", cfg.shape(kind)))
+            for name, shape in names:
+                cnt = int(np.prod(shape))
+                if "norm" in name:
+                    tensors[name] = np.ones(shape, np.float32)
+                else:
+                    reps = -(-cnt // block.size)
+                    tensors[name] = np.tile(block, reps)[:cnt].reshape(shape)
+            path = os.path.join(tempfile.gettempdir(), f"lyk_cpu_baseline_{layers}.safetensors")
+            O.write_safetensors(path, tensors, dtype="F16")
+            del tensors
+            m = O.RefModel(cfg, path)
+            os.remove(path)
+        else:
+            m = O.OracleModel(cfg, threads=1)
+            for kind, layer, arr in m.tensors():
+                arr[...] = 1.0 if kind in (O.T_INPUT_NORM, O.T_POST_NORM, O.T_FINAL_NORM) else \
+                    np.resize(block, arr.size).reshape(arr.shape)
+        s = m.new_seq(16)
+        code, logits = m.prefill(s, [1])
+        t0 = time.perf_counter()
+        for i in range(tokens):
+            code, logits = m.decode(s, 2 + i)
+        times[layers] = (time.perf_counter() - t0) / tokens
+        del m, s
+    per_layer = times[2] - times[1]
+    t_token = times[1] + 27 * per_layer
+    return dict(value=round(1.0 / t_token, 4), unit="tok/s", cores=1,
+                kind="reference" if use_ref else "port",
+                sample=(f"Qwen2.5-7B-architecture decode on the {'reference QwenModel (oracle/_ref)' if use_ref else 'C restatement (oracle)'}, "
+                        f"single thread, {tokens} tokens each with 1 and 2 layers "
+                        f"({times[1]:.2f}s, {times[2]:.2f}s per token); 28 layers extrapolated: "
+                        f"{t_token:.2f}s per token"))
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--quant", choices=["int4", "int8"], default="int4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (single-GPU tier); "
+              "use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    dec = run_decode(args)
+    step_gbs = dec["step_bytes"] / (dec["ms"] * 1e-3) / 1e9
+    log(f"[bench] decode {dec['tok_s']:.1f} tok/s ({dec['ms']:.3f} ms/token, context {dec['ctx_end']}); "
+        f"whole step {step_gbs:.0f} GB/s = {step_gbs / PEAK_HBM_GBS * 100:.1f}% of HBM peak")
+    roof = gemv_roofline(args.quant)
+    log(f"[bench] gate/up GEMV {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        t0 = time.time()
+        cpu = cpu_baseline()
+        log(f"[bench] cpu baseline {cpu['value']} tok/s ({time.time() - t0:.1f}s)")
+    line = {
+        "metric": "decode tok/s Qwen2.5-7B INT4 bs=1 on 1 MI355X; GEMV HBM GB/s vs peak",
+        "value": round(dec["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xfp16" if args.quant == "int4" else "int8xfp16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen2.5-7B-architecture decode, INT4 weight-only (groups of 32, fp16 scales), "
+                        "fp16 activations and KV, batch 1, greedy (GreedyRun)",
+            "prompt_tokens": args.prompt,
+            "decode_tokens": args.steps,
+            "context_at_end": dec["ctx_end"],
+            "quant": args.quant,
+        },
+        "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+        "roofline_kernel": {k: roof[k] for k in ("kernel", "avg_us", "bytes_per_launch")},
+        "step_hbm": {"bytes_per_token": int(dec["step_bytes"]),
+                     "gb_s": round(step_gbs, 1), "frac": round(step_gbs / PEAK_HBM_GBS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

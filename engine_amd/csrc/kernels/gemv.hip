@@ -172,19 +172,26 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(
     uint32_t vmagic;
     asm("v_mov_b32 %0, %1" : "=v"(vmagic) : "s"(magic));
 
+    // Loads are issued in the order their data is used (weights of groups
+    // 0..7, then the scales): vmcnt waits retire in issue order.
     auto load = [&](int c, u32x4 (&w)[8], u32x4& s4) {
-        s4 = st[(size_t)c * 64];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) w[j] = __builtin_nontemporal_load(wt + ((size_t)c * 8 + j) * 64);
+        for (int j = 0; j < 8; ++j) {
+            w[j] = __builtin_nontemporal_load(wt + ((size_t)c * 8 + j) * 64);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        s4 = st[(size_t)c * 64];
+        __builtin_amdgcn_sched_barrier(0);
     };
     auto compute = [&](int c, const u32x4 (&w)[8], const u32x4& s4) {
-        const uint32_t sw[4] = {s4.x, s4.y, s4.z, s4.w};
+        // Group sums first, scales last: the scale vector is the chunk's
+        // last-needed operand, so waiting for it never stalls a group.
+        float gs[M][8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             // Groups past the end of K are packed with scale 0 and code 0;
             // they read the last real group's activations (finite) and add 0.
             const int g = min(c * 8 + j, groups - 1);
-            const float s = h2f(uint16_t(sw[j >> 1] >> (16 * (j & 1))));
             const uint32_t u4[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
             half2_t qa[8], qb[8];
 #pragma unroll
@@ -206,24 +213,39 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(
                     a = dot2(qa[2 * d + 1], as_half2(xg[4 * d + 2]), a);
                     b = dot2(qb[2 * d + 1], as_half2(xg[4 * d + 3]), b);
                 }
-                acc[m] = fmaf(b * 0.0625f + a, s, acc[m]);
+                gs[m][j] = b * 0.0625f + a;
             }
+        }
+        const uint32_t sw[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float s = h2f(uint16_t(sw[j >> 1] >> (16 * (j & 1))));
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[m] = fmaf(gs[m][j], s, acc[m]);
         }
     };
 
     // Two buffers in flight per wave: chunk c+waves is requested before
-    // chunk c is unpacked.
+    // chunk c is unpacked. The request is unconditional (past the end it
+    // re-reads the wave's last chunk) so the number of loads in flight is
+    // the same on every path and the waits before each group stay exact.
     u32x4 wa[8], wb[8], sa, sb;
     int c = c0 + wave;
-    if (c < c1) load(c, wa, sa);
-    while (c < c1) {
-        if (c + waves < c1) load(c + waves, wb, sb);
-        compute(c, wa, sa);
-        c += waves;
-        if (c >= c1) break;
-        if (c + waves < c1) load(c + waves, wa, sa);
-        compute(c, wb, sb);
-        c += waves;
+    if (c < c1) {
+        const int last = c + (c1 - 1 - c) / waves * waves;
+        load(c, wa, sa);
+        while (true) {
+            load(min(c + waves, last), wb, sb);
+            __builtin_amdgcn_sched_barrier(0);  // keep the requests ahead of the math
+            compute(c, wa, sa);
+            c += waves;
+            if (c > last) break;
+            load(min(c + waves, last), wa, sa);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(c, wb, sb);
+            c += waves;
+            if (c > last) break;
+        }
     }
     finish<M, EPI>(acc, tile, split, splits, n, y, ldy, bias, partial, counters, tiles);
 }
@@ -281,15 +303,21 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(
     };
     u32x4 wa[8], wb[8];
     int c = c0 + wave;
-    if (c < c1) load(c, wa);
-    while (c < c1) {
-        if (c + waves < c1) load(c + waves, wb);
-        compute(c, wa);
-        c += waves;
-        if (c >= c1) break;
-        if (c + waves < c1) load(c + waves, wa);
-        compute(c, wb);
-        c += waves;
+    if (c < c1) {
+        const int last = c + (c1 - 1 - c) / waves * waves;
+        load(c, wa);
+        while (true) {
+            load(min(c + waves, last), wb);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(c, wa);
+            c += waves;
+            if (c > last) break;
+            load(min(c + waves, last), wa);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(c, wb);
+            c += waves;
+            if (c > last) break;
+        }
     }
     const float s = h2f(qs[(size_t)tile * 64 + lane]);
 #pragma unroll
