@@ -3,14 +3,16 @@ weight-only decode at batch 1 on one MI355X (BASELINE.json metric, config 4).
 
   python bench.py [--steps K] [--warmup W] [--prompt P] [--quant int4|int8]
 
-A step is one decode token of one sequence (GreedyRun: the whole forward plus
-on-device argmax, replayed as a HIP graph). Weights are random-init
-N(0, 0.02) (synthetic, no checkpoint) quantized at load; the prompt is
-2048 uniform random token ids. One JSON line is printed:
+A step is one decode token of one sequence: one launch of the fused decode
+step kernel (every layer, the LM head and the on-device greedy argmax),
+chained by GreedyRun. Weights are random-init N(0, 0.02) (synthetic, no
+checkpoint) quantized at load; the prompt is P uniform random token ids.
+One JSON line is printed:
   value        decode tokens/s (whole job; one GPU)
-  roofline     the dominant kernel (the fused gate/up INT4 GEMV at 7B shape),
-               algorithmic bytes per launch / average launch time from HIP
-               events, weights rotated over > 2x the 256 MB MALL
+  roofline     the dominant (only) kernel of a step, decode_step_kernel:
+               algorithmic HBM bytes of one launch (packed GEMV weights and
+               scales + K/V of the context, fp16) / its average duration,
+               from HIP events on the model's stream around the timed steps
   cpu_baseline the reference engine's own CPU QwenModel (oracle/_ref), single
                thread as the reference runs it, on a bounded sample (see
                cpu_baseline.sample); the C restatement (oracle) if _ref is absent
@@ -73,62 +75,26 @@ def run_decode(args):
 
     if args.warmup:
         _, tok = greedy(args.warmup, tok)
+    stream = torch.cuda.ExternalStream(hip.stream_ptr)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    ctx0 = seq.length
     t0 = time.perf_counter()
+    e0.record(stream)
     toks, tok = greedy(args.steps, tok)
+    e1.record(stream)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    kernel_us = e0.elapsed_time(e1) * 1e3 / args.steps
     ctx = seq.length
-    # algorithmic bytes of one timed step: the packed GEMV weights + scales,
-    # plus K and V (fp16) of the mean context over the timed steps
+    # algorithmic bytes of one step: the packed GEMV weights + scales, plus
+    # K and V (fp16) of the mean context over the timed steps
     kv_per_ctx = cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
-    step_bytes = hip.gemv_weight_bytes + kv_per_ctx * (ctx - args.steps / 2)
+    step_bytes = hip.gemv_weight_bytes + kv_per_ctx * (ctx0 + ctx + 1) / 2
     gemv_bytes = hip.gemv_weight_bytes
     hip.close()
-    return dict(tok_s=args.steps / dt, ms=dt * 1e3 / args.steps, ctx_end=ctx,
+    return dict(tok_s=args.steps / dt, ms=dt * 1e3 / args.steps, ctx_end=ctx, kernel_us=kernel_us,
                 step_bytes=step_bytes, gemv_bytes=gemv_bytes, tokens=toks)
-
-
-# -------------------------------------------------------- dominant kernel
-def gemv_roofline(quant, reps=200):
-    """Fused gate/up GEMV (Qwen2.5-7B: 2 x [18944, 3584], M=1) timed with HIP
-    events on its launch stream, over weight copies > 2x the MALL."""
-    import torch
-    import engine_amd.lib as L
-    from engine_amd import ops
-
-    n, k = 18944, 3584
-    rng = np.random.default_rng(1)
-    g = (rng.standard_normal((n, k), dtype=np.float32) * 0.02)
-    u = (rng.standard_normal((n, k), dtype=np.float32) * 0.02)
-    pw0 = ops.PackedWeight.from_float(quant, g, u)
-    qw, qs = pw0.qw.cpu().numpy(), pw0.qs.cpu().numpy()
-    copies = max(2, int(np.ceil(640e6 / pw0.nbytes)))
-    pws = [pw0] + [ops.PackedWeight(quant, n, k, qw, qs, True) for _ in range(copies - 1)]
-    x = torch.randn(1, k, device="cuda").half()
-    y = torch.empty((1, n), dtype=torch.float16, device="cuda")
-    ws = ops.Workspace(64 << 20)
-    st = torch.cuda.Stream()
-    fn = L.kernels().lyk_hip_gemv_q4 if quant == "int4" else L.kernels().lyk_hip_gemv_q8
-    sp = ops.stream_ptr(st)
-    argv = [(ops._p(p.qw), ops._p(p.qs), n, k, ops._p(x), k, 1, L.EPI_SILU_F16, ops._p(y), n, None, 0,
-             ops._p(ws.buf), ws.nbytes, sp) for p in pws]
-    for a in argv[:4]:
-        assert fn(*a) == 0
-    st.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for i in range(reps):
-        fn(*argv[i % copies])
-    e1.record(st)
-    st.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
-    alg = pw0.nbytes + k * 2 + n * 2
-    achieved = alg / us / 1e3
-    return dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None,
-                kernel=f"gemv_{quant} gate/up paired 2x[{n},{k}] M=1", avg_us=round(us, 2),
-                bytes_per_launch=alg)
 
 
 # ----------------------------------------------------------- CPU baseline
@@ -206,11 +172,11 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     dec = run_decode(args)
-    step_gbs = dec["step_bytes"] / (dec["ms"] * 1e-3) / 1e9
-    log(f"[bench] decode {dec['tok_s']:.1f} tok/s ({dec['ms']:.3f} ms/token, context {dec['ctx_end']}); "
-        f"whole step {step_gbs:.0f} GB/s = {step_gbs / PEAK_HBM_GBS * 100:.1f}% of HBM peak")
-    roof = gemv_roofline(args.quant)
-    log(f"[bench] gate/up GEMV {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    achieved = dec["step_bytes"] / (dec["kernel_us"] * 1e-6) / 1e9
+    log(f"[bench] decode {dec['tok_s']:.1f} tok/s ({dec['ms']:.3f} ms/token wall, {dec['kernel_us']:.1f} us/step "
+        f"on the stream, context {dec['ctx_end']}); {achieved:.0f} GB/s = {achieved / PEAK_HBM_GBS * 100:.1f}% of HBM peak")
+    roof = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None)
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
@@ -237,10 +203,10 @@ def main():
             "context_at_end": dec["ctx_end"],
             "quant": args.quant,
         },
-        "roofline": {k: roof[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
-        "roofline_kernel": {k: roof[k] for k in ("kernel", "avg_us", "bytes_per_launch")},
-        "step_hbm": {"bytes_per_token": int(dec["step_bytes"]),
-                     "gb_s": round(step_gbs, 1), "frac": round(step_gbs / PEAK_HBM_GBS, 4)},
+        "roofline": roof,
+        "roofline_kernel": {"kernel": f"decode_step_kernel<1, {args.quant}, 128> (fused decode step)",
+                            "avg_us": round(dec["kernel_us"], 2),
+                            "bytes_per_launch": int(dec["step_bytes"])},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -1,5 +1,6 @@
 // C entry points over QwenHipModel (include/lykuro_hip_model.h).
 #include <cmath>
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -44,7 +45,6 @@ HipModelOptions ToOptions(const lyk_model_options* o) {
     opt.kv_pool_tokens = o->kv_pool_tokens;
     if (o->kv_block_tokens) opt.kv_block_tokens = o->kv_block_tokens;
     opt.quantization = o->quant == 1 ? HipWeightQuant::kInt8 : HipWeightQuant::kInt4;
-    opt.use_graphs = o->use_graphs != 0;
     return opt;
 }
 
@@ -159,6 +159,17 @@ uint64_t lyk_model_prefix_cache_hit_tokens(const void* model) {
 }
 uint64_t lyk_model_gemv_weight_bytes(const void* model) {
     return static_cast<const QwenHipModel*>(model)->gemv_weight_bytes();
+}
+void* lyk_model_stream(void* model) { return M(model)->stream(); }
+int32_t lyk_model_set_step_tracing(void* model, int32_t on) {
+    return Code(M(model)->SetStepTracing(on != 0));
+}
+size_t lyk_model_step_trace(void* model, uint64_t* out, size_t max) {
+    std::vector<uint64_t> t;
+    if (!M(model)->StepTrace(t).ok()) return 0;
+    const size_t n = std::min(max, t.size());
+    if (out) std::memcpy(out, t.data(), n * 8);
+    return n;
 }
 
 }  // extern "C"

@@ -29,7 +29,7 @@ namespace lykuro::nie {
 namespace {
 
 constexpr const char kComponent[] = "qwen_hip";
-constexpr int kMaxBatch = 4;          // rows per GEMV pass (lyk_hip_gemv_* limit)
+constexpr int kMaxBatch = 4;          // rows per fused step (lyk_hip_decode_step limit)
 constexpr uint32_t kGreedyMax = 256;  // greedy steps per GreedyRun call
 
 Status HipFail(hipError_t err, const char* what) {
@@ -253,8 +253,6 @@ private:
     std::vector<int> blocks_;
 };
 
-enum class StepMode { kHidden, kLogits, kGreedy };
-
 // Tensor kinds of the synthetic generator's stream ids (kind*1000 + layer).
 enum Kind {
     kEmbed = 0, kInputNorm, kQW, kQB, kKW, kKB, kVW, kVB, kOW, kPostNorm, kGateW, kUpW, kDownW,
@@ -388,33 +386,30 @@ struct QwenHipModel::Impl {
     DevBuf rcos, rsin;
     uint32_t rope_cap = 0, table_stride = 0;
 
-    // decode-step buffers (kMaxBatch rows)
-    int64_t ldx_h = 0, ldx_q = 0, ldx_i = 0, qkv_n = 0;
-    DevBuf d_tokens, d_pos, d_tables, d_h, d_xn, d_attn, d_act, d_qkv, d_q, d_logits, d_ws,
-        d_history, d_step, d_nonfinite, d_prompt;
+    // fused step: model description, its device layer table and workspace
+    lyk_step_model md{};
+    DevBuf d_layers, d_step_ws;
+    uint64_t step_ws_bytes = 0;
+
+    // per-step rows (kMaxBatch)
+    DevBuf d_tokens, d_pos, d_tables, d_logits, d_history, d_step, d_nonfinite, d_prompt;
     PinnedBuf h_tokens, h_pos, h_tables, h_logits, h_history, h_nonfinite, h_prompt;
     size_t prompt_cap = 0;
-    uint64_t ws_bytes = 0;
 
-    std::map<uint64_t, hipGraphExec_t> graphs;
     uint64_t prefix_hits = 0;
     uint64_t gemv_bytes = 0;
+    bool tracing = false;
+    DevBuf d_trace;  // phase timestamps of the last step (when tracing)
 
     ~Impl() {
-        for (auto& [k, g] : graphs) (void)hipGraphExecDestroy(g);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
     uint16_t* kcache(uint32_t l) const { return kv.as<uint16_t>() + (size_t)l * 2 * kv_layer_elems; }
     uint16_t* vcache(uint32_t l) const { return kcache(l) + kv_layer_elems; }
 
-    void DropGraphs() {
-        for (auto& [k, g] : graphs) (void)hipGraphExecDestroy(g);
-        graphs.clear();
-    }
-
     // cos/sin tables and block-table stride for positions < cap; rebuilt
-    // (and cached graphs dropped) when a longer sequence is created.
+    // when a longer sequence is created.
     Status EnsureRope(uint32_t cap) {
         if (cap <= rope_cap) return Status::Ok();
         const uint32_t half = c.head_dim / 2;
@@ -429,111 +424,53 @@ struct QwenHipModel::Impl {
             }
         }
         HIP_OK(hipStreamSynchronize(stream), "device execution failed");
-        DropGraphs();
         Status s = rcos.Upload(cs.data(), cs.size() * 4);
         if (!s.ok()) return s;
         s = rsin.Upload(sn.data(), sn.size() * 4);
         if (!s.ok()) return s;
         rope_cap = cap;
+        md.rope_cos = rcos.as<float>();
+        md.rope_sin = rsin.as<float>();
+        md.rope_positions = int32_t(cap);
         table_stride = std::max<uint32_t>(1, (cap + pool.block_tokens() - 1) / pool.block_tokens());
         s = d_tables.Alloc((size_t)kMaxBatch * table_stride * 4);
         if (!s.ok()) return s;
         return h_tables.Alloc((size_t)kMaxBatch * table_stride * 4);
     }
 
-    Status Gemv(const PackedMat& w, const uint16_t* x, int64_t ldx, int m, int epi, void* y,
-                int64_t ldy, const float* bias) {
-        const int rc = q8 ? lyk_hip_gemv_q8(w.qw.p, w.qs.p, w.n, w.k, x, ldx, m, epi, y, ldy, bias, 0,
-                                            d_ws.p, ws_bytes, stream)
-                          : lyk_hip_gemv_q4(w.qw.p, w.qs.p, w.n, w.k, x, ldx, m, epi, y, ldy, bias, 0,
-                                            d_ws.p, ws_bytes, stream);
-        LYK_OK_OR(rc, "gemv launch failed");
+    // One fused decode step for rows 0..m-1 whose token, position and block
+    // table are already on the device.
+    Status LaunchStep(int m, int mode) {
+        lyk_step_io io{};
+        io.m = m;
+        io.mode = mode;
+        io.tokens = d_tokens.as<int32_t>();
+        io.positions = d_pos.as<int32_t>();
+        io.block_tables = d_tables.as<int32_t>();
+        io.table_stride = int32_t(table_stride);
+        io.logits = d_logits.as<float>();
+        io.ld_logits = c.vocab_size;
+        if (tracing) io.trace = d_trace.as<uint64_t>();
+        if (mode == LYK_STEP_GREEDY) {
+            io.nonfinite = d_nonfinite.as<int32_t>();
+            io.history = d_history.as<int32_t>();
+            io.step = d_step.as<int32_t>();
+        }
+        LYK_OK_OR(lyk_hip_decode_step(&md, &io, d_step_ws.p, step_ws_bytes, kMaxBatch, stream),
+                  "decode step launch failed");
         return Status::Ok();
     }
 
-    static int SplitsFor(uint32_t max_ctx) {
-        if (max_ctx <= 128) return 1;
-        if (max_ctx <= 1024) return 8;
-        if (max_ctx <= 4096) return 16;
-        return 32;
-    }
-
-    // The decode step for rows 0..m-1 whose token, position and block table
-    // are already on the device.
-    Status LaunchStep(int m, int splits, StepMode mode) {
-        const int H = int(c.hidden_size), nq = int(c.num_heads), nkv = int(c.num_kv_heads),
-                  hd = int(c.head_dim);
-        const float eps = c.rms_norm_eps;
-        LYK_OK_OR(lyk_hip_embed_rmsnorm(embed.as<float>(), c.vocab_size, d_tokens.as<int32_t>(), m, H,
-                                        d_h.as<float>(), H, layers[0].input_norm.as<float>(), eps,
-                                        d_xn.as<uint16_t>(), ldx_h, stream),
-                  "embedding launch failed");
-        for (uint32_t l = 0; l < c.num_layers; ++l) {
-            Layer& L = layers[l];
-            Status s = Gemv(L.qkv, d_xn.as<uint16_t>(), ldx_h, m, LYK_EPI_STORE, d_qkv.p, qkv_n,
-                            L.qkv_bias.as<float>());
-            if (!s.ok()) return s;
-            LYK_OK_OR(lyk_hip_rope_kv_append(d_qkv.as<float>(), qkv_n, m, nq, nkv, hd, d_pos.as<int32_t>(),
-                                             rcos.as<float>(), rsin.as<float>(), int(rope_cap),
-                                             d_q.as<float>(), kcache(l), vcache(l), d_tables.as<int32_t>(),
-                                             int(table_stride), int(pool.block_tokens()),
-                                             int(pool.num_blocks()), stream),
-                      "rope launch failed");
-            LYK_OK_OR(lyk_hip_attn_decode(d_q.as<float>(), kcache(l), vcache(l), d_tables.as<int32_t>(),
-                                          int(table_stride), d_pos.as<int32_t>(), m, nq, nkv, hd,
-                                          int(pool.block_tokens()), int(pool.num_blocks()), splits,
-                                          d_attn.as<uint16_t>(), ldx_q, d_ws.p, ws_bytes, stream),
-                      "attention launch failed");
-            s = Gemv(L.o, d_attn.as<uint16_t>(), ldx_q, m, LYK_EPI_ADD, d_h.p, H, nullptr);
-            if (!s.ok()) return s;
-            LYK_OK_OR(lyk_hip_rmsnorm_f16(d_h.as<float>(), H, L.post_norm.as<float>(), eps, m, H,
-                                          d_xn.as<uint16_t>(), ldx_h, stream),
-                      "rmsnorm launch failed");
-            s = Gemv(L.gateup, d_xn.as<uint16_t>(), ldx_h, m, LYK_EPI_SILU_F16, d_act.p, ldx_i, nullptr);
-            if (!s.ok()) return s;
-            s = Gemv(L.down, d_act.as<uint16_t>(), ldx_i, m, LYK_EPI_ADD, d_h.p, H, nullptr);
-            if (!s.ok()) return s;
-            const float* next_norm =
-                l + 1 < c.num_layers ? layers[l + 1].input_norm.as<float>() : final_norm.as<float>();
-            LYK_OK_OR(lyk_hip_rmsnorm_f16(d_h.as<float>(), H, next_norm, eps, m, H, d_xn.as<uint16_t>(),
-                                          ldx_h, stream),
-                      "rmsnorm launch failed");
+    // After a stream synchronization: a step that could not complete leaves
+    // an error word in the workspace; reset it so later steps can run.
+    Status CheckSteps() {
+        int32_t err = 0;
+        LYK_OK_OR(lyk_hip_step_error(d_step_ws.p, &err, stream), "decode step status read failed");
+        if (err != 0) {
+            (void)lyk_hip_step_reset(d_step_ws.p, step_ws_bytes, stream);
+            (void)hipStreamSynchronize(stream);
+            return Status(ErrorCode::kGpuUnhealthy, "decode step did not complete on the device", kComponent);
         }
-        if (mode == StepMode::kHidden) return Status::Ok();
-        Status s = Gemv(lm_head, d_xn.as<uint16_t>(), ldx_h, m, LYK_EPI_STORE, d_logits.p, c.vocab_size,
-                        nullptr);
-        if (!s.ok()) return s;
-        if (mode == StepMode::kGreedy)
-            LYK_OK_OR(lyk_hip_argmax(d_logits.as<float>(), c.vocab_size, 1, c.vocab_size,
-                                     d_tokens.as<int32_t>(), d_nonfinite.as<int32_t>(), d_pos.as<int32_t>(),
-                                     d_history.as<int32_t>(), d_step.as<int32_t>(), d_ws.p, ws_bytes,
-                                     stream),
-                      "argmax launch failed");
-        return Status::Ok();
-    }
-
-    // Runs one step, through a cached HIP graph when enabled.
-    Status RunStep(int m, int splits, StepMode mode) {
-        if (!opt.use_graphs) return LaunchStep(m, splits, mode);
-        const uint64_t key = (uint64_t(m) << 32) | (uint64_t(splits) << 8) | uint64_t(mode);
-        auto it = graphs.find(key);
-        if (it == graphs.end()) {
-            HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "graph capture failed");
-            Status s = LaunchStep(m, splits, mode);
-            hipGraph_t g = nullptr;
-            const hipError_t e = hipStreamEndCapture(stream, &g);
-            if (!s.ok()) {
-                if (g) (void)hipGraphDestroy(g);
-                return s;
-            }
-            if (e != hipSuccess) return HipFail(e, "graph capture failed");
-            hipGraphExec_t exec = nullptr;
-            const hipError_t ie = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(g);
-            if (ie != hipSuccess) return HipFail(ie, "graph instantiation failed");
-            it = graphs.emplace(key, exec).first;
-        }
-        HIP_OK(hipGraphLaunch(it->second, stream), "graph launch failed");
         return Status::Ok();
     }
 
@@ -618,10 +555,8 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
     model->limits_.max_context_tokens = c.max_context_tokens;
     model->limits_.eos_token_ids = c.eos_token_ids;
     model->device_id_ = options.device_id;
-    if (options.kv_block_tokens == 0 || c.head_dim > 512 || c.num_heads / c.num_kv_heads > 16 ||
-        (c.num_heads / c.num_kv_heads) * c.head_dim > 4096) {
-        r.status = Status(ErrorCode::kUnsupportedModel, "model geometry unsupported by the hip kernels",
-                          kComponent);
+    if (options.kv_block_tokens == 0) {
+        r.status = Status(ErrorCode::kUnsupportedModel, "kv block size must be positive", kComponent);
         return r;
     }
 
@@ -672,7 +607,8 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
         LOAD_OR_RETURN(UploadF32(a, L.input_norm));
         LOAD_OR_RETURN(read(LayerName(l, "post_attention_layernorm.weight"), {H}, a));
         LOAD_OR_RETURN(UploadF32(a, L.post_norm));
-        // fused qkv: rows [q | k | v], bias concatenated the same way
+        // fused qkv: rows [q | k | v] in the step kernel's RoPE-pair order
+        // (lyk_qkv_rope_order), bias in the same order
         std::vector<float> qkv, bias, t;
         LOAD_OR_RETURN(read(LayerName(l, "self_attn.q_proj.weight"), {qd, H}, t));
         qkv.insert(qkv.end(), t.begin(), t.end());
@@ -683,6 +619,18 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
         for (const char* nm : {"self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias"}) {
             LOAD_OR_RETURN(read(LayerName(l, nm), {std::string(nm).find("q_proj") != std::string::npos ? qd : kvd}, t));
             bias.insert(bias.end(), t.begin(), t.end());
+        }
+        {
+            const size_t rows = size_t(qd + 2 * kvd);
+            std::vector<int32_t> perm(rows);
+            lyk_qkv_rope_order(int(c.num_heads), int(c.num_kv_heads), int(c.head_dim), perm.data());
+            std::vector<float> pq(qkv.size()), pb(rows);
+            for (size_t r2 = 0; r2 < rows; ++r2) {
+                std::copy_n(qkv.begin() + size_t(perm[r2]) * H, H, pq.begin() + r2 * H);
+                pb[r2] = bias[size_t(perm[r2])];
+            }
+            qkv.swap(pq);
+            bias.swap(pb);
         }
         LOAD_OR_RETURN(QuantizeUpload(I.q8, qkv, nullptr, int64_t(qd + 2 * kvd), int64_t(H), L.qkv, I.gemv_bytes));
         LOAD_OR_RETURN(UploadF32(bias, L.qkv_bias));
@@ -719,43 +667,69 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
     I.kv_layer_elems = (size_t)nblocks * c.num_kv_heads * bt * c.head_dim;
     LOAD_OR_RETURN(I.kv.Alloc(I.kv_layer_elems * 2 * 2 * c.num_layers));
 
-    // step buffers
-    I.ldx_h = RoundUp(H, 32);
-    I.ldx_q = RoundUp(int64_t(qd), 32);
-    I.ldx_i = RoundUp(int64_t(In), 32);
-    I.qkv_n = int64_t(qd + 2 * kvd);
+    // step rows
     const size_t B = kMaxBatch;
     LOAD_OR_RETURN(I.d_tokens.Alloc(B * 4));
     LOAD_OR_RETURN(I.d_pos.Alloc(B * 4));
-    LOAD_OR_RETURN(I.d_h.Alloc(B * H * 4));
-    LOAD_OR_RETURN(I.d_xn.Alloc(B * I.ldx_h * 2));
-    LOAD_OR_RETURN(I.d_attn.Alloc(B * I.ldx_q * 2));
-    LOAD_OR_RETURN(I.d_act.Alloc(B * I.ldx_i * 2));
-    LOAD_OR_RETURN(I.d_qkv.Alloc(B * I.qkv_n * 4));
-    LOAD_OR_RETURN(I.d_q.Alloc(B * qd * 4));
     LOAD_OR_RETURN(I.d_logits.Alloc(B * V * 4));
     LOAD_OR_RETURN(I.d_history.Alloc(kGreedyMax * 4));
     LOAD_OR_RETURN(I.d_step.Alloc(4));
     LOAD_OR_RETURN(I.d_nonfinite.Alloc(B * 4));
-    // workspace: the largest need of any launch of the step (they run one
-    // after another on the stream and leave it zeroed)
-    uint64_t ws = lyk_hip_argmax_workspace_bytes(1, V);
-    for (int m = 1; m <= kMaxBatch; ++m) {
-        const Impl::Layer& L = I.layers[0];
-        const PackedMat* mats[] = {&L.qkv, &L.o, &L.down, &I.lm_head};
-        for (const PackedMat* w : mats)
-            ws = std::max(ws, lyk_hip_gemv_workspace_bytes(w->n, w->k, m, 0, 0, I.q8));
-        ws = std::max(ws, lyk_hip_gemv_workspace_bytes(L.gateup.n, L.gateup.k, m, 0, 1, I.q8));
-        ws = std::max(ws, lyk_hip_attn_workspace_bytes(m, c.num_heads, c.num_kv_heads, c.head_dim, 32));
-    }
-    I.ws_bytes = ws;
-    LOAD_OR_RETURN(I.d_ws.Alloc(ws));
     LOAD_OR_RETURN(I.h_tokens.Alloc(B * 4));
     LOAD_OR_RETURN(I.h_pos.Alloc(B * 4));
     LOAD_OR_RETURN(I.h_logits.Alloc(B * V * 4));
     LOAD_OR_RETURN(I.h_history.Alloc(kGreedyMax * 4));
     LOAD_OR_RETURN(I.h_nonfinite.Alloc(B * 4));
+
+    // fused step: model description, device layer table, workspace
+    std::vector<lyk_step_layer> table(c.num_layers);
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        const Impl::Layer& L = I.layers[l];
+        lyk_step_layer& e = table[l];
+        e.qkv_w = L.qkv.qw.p;
+        e.qkv_s = L.qkv.qs.p;
+        e.qkv_bias = L.qkv_bias.as<float>();
+        e.o_w = L.o.qw.p;
+        e.o_s = L.o.qs.p;
+        e.gateup_w = L.gateup.qw.p;
+        e.gateup_s = L.gateup.qs.p;
+        e.down_w = L.down.qw.p;
+        e.down_s = L.down.qs.p;
+        e.input_norm = L.input_norm.as<float>();
+        e.post_norm = L.post_norm.as<float>();
+        e.k_cache = I.kcache(l);
+        e.v_cache = I.vcache(l);
+    }
+    LOAD_OR_RETURN(I.d_layers.Upload(table.data(), table.size() * sizeof(lyk_step_layer)));
+    lyk_step_model& md = I.md;
+    md.vocab_size = int32_t(V);
+    md.hidden_size = int32_t(H);
+    md.num_layers = int32_t(c.num_layers);
+    md.num_heads = int32_t(c.num_heads);
+    md.num_kv_heads = int32_t(c.num_kv_heads);
+    md.head_dim = int32_t(c.head_dim);
+    md.intermediate_size = int32_t(In);
+    md.q8 = I.q8 ? 1 : 0;
+    md.rms_norm_eps = c.rms_norm_eps;
+    md.block_tokens = int32_t(bt);
+    md.num_blocks = int32_t(nblocks);
+    md.embed = I.embed.as<float>();
+    md.final_norm = I.final_norm.as<float>();
+    md.lm_head_w = I.lm_head.qw.p;
+    md.lm_head_s = I.lm_head.qs.p;
+    md.layers = I.d_layers.as<lyk_step_layer>();
     LOAD_OR_RETURN(I.EnsureRope(std::max(1u, c.max_context_tokens)));
+    I.step_ws_bytes = lyk_hip_step_workspace_bytes(&md, kMaxBatch);
+    if (I.step_ws_bytes == 0) {
+        r.status = Status(ErrorCode::kUnsupportedModel, "model geometry unsupported by the hip kernels",
+                          kComponent);
+        return r;
+    }
+    LOAD_OR_RETURN(I.d_step_ws.Alloc(I.step_ws_bytes, false));
+    if (lyk_hip_step_reset(I.d_step_ws.p, I.step_ws_bytes, I.stream) != LYK_OK) {
+        r.status = Status(ErrorCode::kGpuUnhealthy, "workspace reset failed", kComponent);
+        return r;
+    }
     if (hipDeviceSynchronize() != hipSuccess) {
         r.status = Status(ErrorCode::kGpuUnhealthy, "device initialisation failed", kComponent);
         return r;
@@ -768,6 +742,30 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
 
 QwenHipModel::~QwenHipModel() {
     if (impl_) (void)hipSetDevice(device_id_);
+}
+
+void* QwenHipModel::stream() const { return impl_->stream; }
+
+Status QwenHipModel::SetStepTracing(bool on) {
+    HIP_OK(hipSetDevice(device_id_), "hip device not usable");
+    Impl& I = *impl_;
+    if (on && !I.d_trace.p) {
+        Status s = I.d_trace.Alloc((4 * (size_t)lyk_hip_step_barriers(&I.md, LYK_STEP_GREEDY) + 2) * 8);
+        if (!s.ok()) return s;
+    }
+    I.tracing = on;
+    return Status::Ok();
+}
+
+Status QwenHipModel::StepTrace(std::vector<uint64_t>& ticks) {
+    Impl& I = *impl_;
+    ticks.clear();
+    if (!I.d_trace.p) return Status(ErrorCode::kInvalidRequest, "step tracing is off", kComponent);
+    HIP_OK(hipSetDevice(device_id_), "hip device not usable");
+    HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+    ticks.resize(I.d_trace.bytes / 8);
+    HIP_OK(hipMemcpy(ticks.data(), I.d_trace.p, I.d_trace.bytes, hipMemcpyDeviceToHost), "trace download failed");
+    return Status::Ok();
 }
 
 uint32_t QwenHipModel::kv_blocks_total() const { return impl_->pool.num_blocks(); }
@@ -857,7 +855,7 @@ Status QwenHipModel::Prefill(SequenceState& state, const std::vector<uint32_t>& 
             HIP_OK(hipMemcpyAsync(I.d_pos.p, row + 1, 4, hipMemcpyDeviceToDevice, I.stream),
                    "position copy failed");
             const bool last = i + 1 == n;
-            s = I.RunStep(1, Impl::SplitsFor(i + 1), last ? StepMode::kLogits : StepMode::kHidden);
+            s = I.LaunchStep(1, last ? LYK_STEP_LOGITS : LYK_STEP_HIDDEN);
             if (!s.ok()) return s;
         }
         seq.Advance(n - start);
@@ -866,6 +864,10 @@ Status QwenHipModel::Prefill(SequenceState& state, const std::vector<uint32_t>& 
     HIP_OK(hipMemcpyAsync(I.h_logits.p, I.d_logits.p, logits.size() * 4, hipMemcpyDeviceToHost, I.stream),
            "logits download failed");
     HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+    {
+        Status st = I.CheckSteps();
+        if (!st.ok()) return st;
+    }
     std::memcpy(logits.data(), I.h_logits.p, logits.size() * 4);
 
     if (seq.options().allow_prefix_cache)
@@ -907,22 +909,22 @@ Status QwenHipModel::DecodeBatch(std::vector<DecodeBatchItem>& items, std::vecto
         const size_t m = std::min<size_t>(kMaxBatch, valid.size() - g0);
         std::vector<HipSequenceState*> seqs;
         std::vector<uint32_t> toks, pos;
-        uint32_t max_ctx = 0;
         for (size_t i = 0; i < m; ++i) {
             const size_t idx = valid[g0 + i];
             auto* st = static_cast<HipSequenceState*>(items[idx].state);
             seqs.push_back(st);
             toks.push_back(items[idx].token);
             pos.push_back(st->length());
-            max_ctx = std::max(max_ctx, st->length() + 1);
         }
         Status s = I.UploadRows(seqs, toks, pos);
         if (!s.ok()) return s;
-        s = I.RunStep(int(m), Impl::SplitsFor(max_ctx), StepMode::kLogits);
+        s = I.LaunchStep(int(m), LYK_STEP_LOGITS);
         if (!s.ok()) return s;
         HIP_OK(hipMemcpyAsync(I.h_logits.p, I.d_logits.p, m * V * 4, hipMemcpyDeviceToHost, I.stream),
                "logits download failed");
         HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+        s = I.CheckSteps();
+        if (!s.ok()) return s;
         const float* hl = I.h_logits.as<float>();
         for (size_t i = 0; i < m; ++i) {
             const size_t idx = valid[g0 + i];
@@ -962,10 +964,8 @@ Status QwenHipModel::GreedyRun(SequenceState& state, uint32_t token, uint32_t ma
     if (!s.ok()) return s;
     HIP_OK(hipMemsetAsync(I.d_step.p, 0, 4, I.stream), "step reset failed");
     HIP_OK(hipMemsetAsync(I.d_nonfinite.p, 0, 4, I.stream), "flag reset failed");
-    // one split count for the whole run, sized for its final context
-    const int splits = Impl::SplitsFor(len + steps);
     for (uint32_t i = 0; i < steps; ++i) {
-        s = I.RunStep(1, splits, StepMode::kGreedy);
+        s = I.LaunchStep(1, LYK_STEP_GREEDY);
         if (!s.ok()) return s;
     }
     HIP_OK(hipMemcpyAsync(I.h_history.p, I.d_history.p, steps * 4, hipMemcpyDeviceToHost, I.stream),
@@ -973,6 +973,8 @@ Status QwenHipModel::GreedyRun(SequenceState& state, uint32_t token, uint32_t ma
     HIP_OK(hipMemcpyAsync(I.h_nonfinite.p, I.d_nonfinite.p, 4, hipMemcpyDeviceToHost, I.stream),
            "flag download failed");
     HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+    s = I.CheckSteps();
+    if (!s.ok()) return s;
     if (I.h_nonfinite.as<int32_t>()[0] != 0)
         return Status(ErrorCode::kInferenceFailed, "logits contain non-finite values", kComponent);
     const int32_t* hist = I.h_history.as<int32_t>();

@@ -9,9 +9,10 @@
 //
 // Weights are quantized at load (int4 in groups of 32 with fp16 scales, or
 // int8 per output row with fp16 scales) and repacked into the tile layouts
-// of include/lykuro_hip.h; activations between kernels are fp16, the
-// residual stream and logits fp32, the paged KV cache fp16. Every device
-// computation is one of the hand-written gfx950 kernels behind the C ABI.
+// of include/lykuro_hip.h; GEMV inputs are fp16, the residual stream and
+// logits fp32, the paged KV cache fp16. Each decode step (one token of up to
+// four sequences) is one launch of the fused gfx950 step kernel behind the C
+// ABI (lyk_hip_decode_step).
 #pragma once
 
 #include <cstdint>
@@ -38,8 +39,6 @@ struct HipModelOptions {
     uint32_t kv_pool_tokens = 0;
     uint32_t kv_block_tokens = 16;
     HipWeightQuant quantization = HipWeightQuant::kInt4;
-    // Replay the decode step as a HIP graph (off: direct launches).
-    bool use_graphs = true;
 };
 
 // fp32 weights by reference tensor name. The safetensors file is one source;
@@ -136,6 +135,13 @@ public:
     uint64_t prefix_cache_hit_tokens() const;
     // Bytes of quantized GEMV weights streamed per decode token.
     uint64_t gemv_weight_bytes() const;
+    // Phase timeline of the fused step (profiling): when on, every step
+    // records device timestamps (see lyk_step_io::trace); StepTrace returns
+    // those of the most recent step.
+    Status SetStepTracing(bool on);
+    // The HIP stream (hipStream_t) all device work of the model runs on.
+    void* stream() const;
+    Status StepTrace(std::vector<uint64_t>& ticks);
 
     struct Impl;
 

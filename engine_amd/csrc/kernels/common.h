@@ -50,6 +50,25 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Global-memory view of a generic pointer. Pointers that reach a kernel
+// through a struct in device memory lose their address space; accesses
+// through them would compile to flat instructions, which also count against
+// the LDS wait counter and so serialize LDS reads behind outstanding global
+// loads.
+#define LYK_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ LYK_GLOBAL T* gp(T* p) {
+    return (LYK_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ T ld(const T* p) {
+    return *gp(p);
+}
+template <class T>
+__device__ __forceinline__ void st(T* p, T v) {
+    *gp(p) = v;
+}
+
 // Publishes this wave's earlier agent-scope (sc1) atomic stores before a
 // following arrival counter update: s_waitcnt 0 returns only once those
 // stores are performed at the device coherence point. (A workgroup-scope
@@ -65,16 +84,18 @@ __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected
     publish_sc1_stores();
     unsigned prev = 0;
     if ((threadIdx.x & 63) == 0)
-        prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __hip_atomic_fetch_add(gp(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     prev = __shfl(prev, 0, 64);
     return prev == expected - 1;
 }
 
-__device__ __forceinline__ void store_sc1(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <class T>
+__device__ __forceinline__ void store_sc1(T* p, T v) {
+    __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float load_sc1(float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <class T>
+__device__ __forceinline__ T load_sc1(const T* p) {
+    return __hip_atomic_load(gp(const_cast<T*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }

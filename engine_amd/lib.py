@@ -57,6 +57,12 @@ _KERNEL_SIGS = {
     "lyk_hip_gemv_splits": (I, [I64, I64, I, I, I]),
     "lyk_hip_gemv_q4": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
     "lyk_hip_gemv_q8": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
+    "lyk_hip_step_workspace_bytes": (U64, [P, I]),
+    "lyk_hip_step_barriers": (U32, [P, I]),
+    "lyk_hip_decode_step": (I, [P, P, P, U64, I, P]),
+    "lyk_hip_step_reset": (I, [P, U64, P]),
+    "lyk_hip_step_error": (I, [P, C.POINTER(C.c_int32), P]),
+    "lyk_qkv_rope_order": (None, [I, I, I, P]),
 }
 
 class ModelConfig(C.Structure):
@@ -69,7 +75,7 @@ class ModelConfig(C.Structure):
 
 class ModelOptions(C.Structure):
     _fields_ = [("device_id", C.c_int32), ("kv_pool_tokens", C.c_uint32),
-                ("kv_block_tokens", C.c_uint32), ("quant", C.c_int32), ("use_graphs", C.c_int32)]
+                ("kv_block_tokens", C.c_uint32), ("quant", C.c_int32)]
 
 
 I32P = C.POINTER(C.c_int32)
@@ -89,6 +95,9 @@ _MODEL_SIGS = {
     "lyk_model_kv_blocks_free": (U32, [P]),
     "lyk_model_prefix_cache_hit_tokens": (U64, [P]),
     "lyk_model_gemv_weight_bytes": (U64, [P]),
+    "lyk_model_set_step_tracing": (C.c_int32, [P, C.c_int32]),
+    "lyk_model_stream": (P, [P]),
+    "lyk_model_step_trace": (C.c_size_t, [P, P, C.c_size_t]),
     "lyk_synth_normal": (None, [U64, U64, U64, U64, F, P]),
 }
 

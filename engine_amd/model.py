@@ -41,11 +41,10 @@ class Options:
     kv_pool_tokens: int = 0
     kv_block_tokens: int = 16
     quant: str = "int4"
-    use_graphs: bool = True
 
     def c(self):
         return L.ModelOptions(self.device_id, self.kv_pool_tokens, self.kv_block_tokens,
-                              1 if self.quant == "int8" else 0, int(self.use_graphs))
+                              1 if self.quant == "int8" else 0)
 
 
 class HipModel:
@@ -136,6 +135,22 @@ class HipModel:
     @property
     def gemv_weight_bytes(self):
         return L.model_lib().lyk_model_gemv_weight_bytes(self._h)
+
+    @property
+    def stream_ptr(self):
+        """hipStream_t of the model (for torch.cuda.ExternalStream)."""
+        return L.model_lib().lyk_model_stream(self._h)
+
+    def set_step_tracing(self, on=True):
+        L.check("lyk_model_set_step_tracing", L.model_lib().lyk_model_set_step_tracing(self._h, int(on)))
+
+    def step_trace(self):
+        """Device timestamps (100 MHz ticks) of the latest step: entry,
+        after each grid barrier, exit, then the arrivals at each barrier."""
+        n = 4 * (5 * self.cfg.num_layers + 1) + 2
+        buf = (C.c_uint64 * n)()
+        got = L.model_lib().lyk_model_step_trace(self._h, buf, n)
+        return list(buf)[:got]
 
 
 class Sequence:

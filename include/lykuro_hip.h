@@ -206,6 +206,103 @@ int lyk_hip_argmax(const float* d_logits, int64_t ldl, int m, int64_t n,
                    int32_t* d_history, int32_t* d_step, void* d_workspace,
                    uint64_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------- fused decode step
+ * One decode step of a Qwen2 model (embedding, every layer, final norm, LM
+ * head, greedy argmax) as a single persistent cooperative launch of one
+ * workgroup per CU; replaces the per-step kernel sequence of
+ * QwenCudaModel::Decode / DecodeBatch / GreedyRun
+ * (qwen_cuda_model.cu:2641-2776, 2778-3102), whose CPU counterpart is
+ * QwenModel::Forward (qwen_model.cpp:216-331). Arithmetic per op is that of
+ * the entry points above (same quantized formats, fp16 activations into each
+ * GEMV, fp32 residual stream and softmax, fp16 KV cache).
+ *
+ * Weights: packed as above; qkv is one [(nq+2nkv)*hd, hidden] matrix in the
+ * row order lyk_qkv_rope_order gives (bias in the same order), gate/up is a
+ * paired packing (A = gate, B = up). The layer table is a device array. */
+typedef struct lyk_step_layer {
+    const void* qkv_w;
+    const void* qkv_s;
+    const float* qkv_bias;  /* fp32 [(nq+2nkv)*hd], rope row order */
+    const void* o_w;
+    const void* o_s;
+    const void* gateup_w;
+    const void* gateup_s;
+    const void* down_w;
+    const void* down_s;
+    const float* input_norm;
+    const float* post_norm;
+    uint16_t* k_cache;      /* fp16 [num_blocks][nkv][block_tokens][hd] */
+    uint16_t* v_cache;
+} lyk_step_layer;
+
+typedef struct lyk_step_model {
+    int32_t vocab_size, hidden_size, num_layers, num_heads, num_kv_heads, head_dim,
+        intermediate_size;
+    int32_t q8;              /* 0: int4 weights, 1: int8 weights */
+    float rms_norm_eps;
+    int32_t block_tokens, num_blocks;
+    int32_t rope_positions;  /* rows of the cos/sin tables */
+    const float* embed;      /* fp32 [vocab][hidden] */
+    const float* final_norm;
+    const void* lm_head_w;
+    const void* lm_head_s;
+    const lyk_step_layer* layers;  /* device array [num_layers] */
+    const float* rope_cos;   /* fp32 [rope_positions][hd/2] */
+    const float* rope_sin;
+} lyk_step_model;
+
+enum {
+    LYK_STEP_HIDDEN = 0,  /* KV append only (prompt tokens before the last) */
+    LYK_STEP_LOGITS = 1,  /* + logits of every row */
+    LYK_STEP_GREEDY = 2,  /* + on-device greedy token (m == 1) */
+};
+
+typedef struct lyk_step_io {
+    int32_t m;                    /* batch rows, 1..4 */
+    int32_t mode;
+    int32_t* tokens;              /* device [m]; GREEDY: replaced by the chosen token */
+    int32_t* positions;           /* device [m]; GREEDY: advanced by one */
+    const int32_t* block_tables;  /* device [m][table_stride] */
+    int32_t table_stride;
+    float* logits;                /* device [m][ld_logits] (LOGITS, GREEDY) */
+    int64_t ld_logits;
+    int32_t* nonfinite;           /* GREEDY, optional: += non-finite logits */
+    int32_t* history;             /* GREEDY, optional: history[*step] = token, */
+    int32_t* step;                /*   ++*step (the GreedyRun chaining) */
+    uint64_t* trace;              /* optional, 4*barriers + 2 values: s_memrealtime
+                                     ticks (100 MHz) of workgroup 0 at entry [0],
+                                     leaving barrier i [1+i], at exit
+                                     [barriers+1], arriving at barrier i
+                                     [barriers+2+i], phase i's inputs ready
+                                     [2*barriers+2+i], its main loop done
+                                     [3*barriers+2+i] */
+} lyk_step_io;
+
+/* Workspace for steps of up to max_rows rows (0 if the geometry is
+ * unsupported). Prepare it with lyk_hip_step_reset before the first step;
+ * afterwards every step leaves it valid for the next on the same stream. */
+uint64_t lyk_hip_step_workspace_bytes(const lyk_step_model* model, int max_rows);
+/* Grid barriers one step of `mode` performs. */
+uint32_t lyk_hip_step_barriers(const lyk_step_model* model, int mode);
+/* Launches one step (stream-ordered, asynchronous). Positions must be
+ * < rope_positions and have their blocks in the tables; the host checks
+ * both. The launch arguments are kept in the workspace and uploaded only when
+ * they change. A step whose grid could not complete (a wait exceeding ~2 s)
+ * sets the workspace's error word and makes later steps exit at once: read it
+ * with lyk_hip_step_error and, if set, call lyk_hip_step_reset. */
+int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io,
+                        void* d_workspace, uint64_t workspace_bytes, int max_rows,
+                        void* stream);
+/* Zeroes the workspace (stream-ordered) and forgets its cached arguments. */
+int lyk_hip_step_reset(void* d_workspace, uint64_t workspace_bytes, void* stream);
+/* Copies the error word (0 = no error) to *error_out and waits for it. */
+int lyk_hip_step_error(const void* d_workspace, int32_t* error_out, void* stream);
+/* Row order of the packed qkv matrix: packed row r holds natural row
+ * perm[r] of [q | k | v]. Heads of hd > 64 are stored in blocks of 64 rows
+ * that hold 32 RoPE pairs (dims d and d + hd/2 in rows j and j + 32);
+ * smaller heads keep the natural order. */
+void lyk_qkv_rope_order(int nq, int nkv, int hd, int32_t* perm);
+
 int lyk_abi_version(void);
 
 #ifdef __cplusplus

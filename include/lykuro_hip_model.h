@@ -38,7 +38,6 @@ typedef struct lyk_model_options {
     uint32_t kv_pool_tokens;
     uint32_t kv_block_tokens;
     int32_t quant;
-    int32_t use_graphs;
 } lyk_model_options;
 
 /* QwenHipModel::Load from a safetensors file (replaces QwenCudaModel::Load,
@@ -77,6 +76,14 @@ uint32_t lyk_model_kv_blocks_free(const void* model);
 uint64_t lyk_model_prefix_cache_hit_tokens(const void* model);
 /* Bytes of packed GEMV weights (+ scales) streamed per decode token. */
 uint64_t lyk_model_gemv_weight_bytes(const void* model);
+/* Profiling: record the phase timeline of every step (lyk_step_io::trace);
+ * lyk_model_step_trace copies that of the latest step (up to max values,
+ * returns the count; 0 when tracing is off). */
+int32_t lyk_model_set_step_tracing(void* model, int32_t on);
+/* The hipStream_t (as void*) every device operation of the model runs on,
+ * for callers that time it with events. */
+void* lyk_model_stream(void* model);
+size_t lyk_model_step_trace(void* model, uint64_t* out, size_t max);
 
 /* Seeded N(0, sigma^2) stream: value i of stream `stream` depends only on
  * (seed, stream, i); Box-Muller on splitmix64 outputs. */
