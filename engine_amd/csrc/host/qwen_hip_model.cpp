@@ -607,8 +607,7 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
         LOAD_OR_RETURN(UploadF32(a, L.input_norm));
         LOAD_OR_RETURN(read(LayerName(l, "post_attention_layernorm.weight"), {H}, a));
         LOAD_OR_RETURN(UploadF32(a, L.post_norm));
-        // fused qkv: rows [q | k | v] in the step kernel's RoPE-pair order
-        // (lyk_qkv_rope_order), bias in the same order
+        // fused qkv: rows [q | k | v], bias concatenated the same way
         std::vector<float> qkv, bias, t;
         LOAD_OR_RETURN(read(LayerName(l, "self_attn.q_proj.weight"), {qd, H}, t));
         qkv.insert(qkv.end(), t.begin(), t.end());
@@ -619,18 +618,6 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
         for (const char* nm : {"self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias"}) {
             LOAD_OR_RETURN(read(LayerName(l, nm), {std::string(nm).find("q_proj") != std::string::npos ? qd : kvd}, t));
             bias.insert(bias.end(), t.begin(), t.end());
-        }
-        {
-            const size_t rows = size_t(qd + 2 * kvd);
-            std::vector<int32_t> perm(rows);
-            lyk_qkv_rope_order(int(c.num_heads), int(c.num_kv_heads), int(c.head_dim), perm.data());
-            std::vector<float> pq(qkv.size()), pb(rows);
-            for (size_t r2 = 0; r2 < rows; ++r2) {
-                std::copy_n(qkv.begin() + size_t(perm[r2]) * H, H, pq.begin() + r2 * H);
-                pb[r2] = bias[size_t(perm[r2])];
-            }
-            qkv.swap(pq);
-            bias.swap(pb);
         }
         LOAD_OR_RETURN(QuantizeUpload(I.q8, qkv, nullptr, int64_t(qd + 2 * kvd), int64_t(H), L.qkv, I.gemv_bytes));
         LOAD_OR_RETURN(UploadF32(bias, L.qkv_bias));
@@ -750,7 +737,8 @@ Status QwenHipModel::SetStepTracing(bool on) {
     HIP_OK(hipSetDevice(device_id_), "hip device not usable");
     Impl& I = *impl_;
     if (on && !I.d_trace.p) {
-        Status s = I.d_trace.Alloc((4 * (size_t)lyk_hip_step_barriers(&I.md, LYK_STEP_GREEDY) + 2) * 8);
+        Status s = I.d_trace.Alloc((size_t)lyk_hip_step_grid() *
+                                   (4 * (size_t)lyk_hip_step_phases(&I.md, LYK_STEP_GREEDY) + 2) * 8);
         if (!s.ok()) return s;
     }
     I.tracing = on;

@@ -1,8 +1,8 @@
 // The whole decode step of a Qwen2 model as one persistent, cooperative
-// launch on gfx950: embedding, every layer (RMSNorm, fused QKV GEMV with bias
-// + RoPE + paged KV append, GQA attention, O GEMV + residual, RMSNorm,
-// gate/up GEMV + SiLU, down GEMV + residual), the final norm, the LM head and
-// the greedy argmax.
+// launch on gfx950: embedding, every layer (RMSNorm, fused QKV GEMV, bias +
+// RoPE + paged KV append, GQA attention, O GEMV + residual, RMSNorm, gate/up
+// GEMV + SiLU, down GEMV + residual), the final norm, the LM head and the
+// greedy argmax.
 //
 // Reference: one QwenCudaModel::Decode / DecodeBatch / GreedyRun step
 // (backends/cuda/qwen_cuda_model.cu:2641-2776, 2778-3102), whose CPU
@@ -11,39 +11,42 @@
 // on MI355X each kernel boundary costs a launch, a ramp-up/drain of 256 CUs
 // and an L2 write-back across 8 XCDs, which at batch 1 costs more than the
 // weights take to stream. Here one workgroup per CU stays resident for the
-// whole step and phases hand over through device-scope counters.
+// whole step.
 //
-// Phases and hand-over
-//   * GEMV phases use a stream-K split: the (row tile, K chunk) space of the
-//     matrix is cut into one contiguous range per workgroup, and each
-//     workgroup's range into one contiguous range per wave, so every CU
-//     streams the same number of bytes whatever the matrix shape. A tile
-//     finished inside one workgroup goes straight to its epilogue; a tile
-//     shared by several workgroups is finished by the last of them to arrive
-//     (per-tile counter), which adds the partials in workgroup order.
-//   * The activation vector of a GEMV phase sits in LDS (only the K chunks
-//     the workgroup's range touches), written by the phase prologue: an
-//     RMSNorm every workgroup computes for itself from the fp32 residual
-//     stream, or a copy of the fp16 attention / MLP activations.
-//   * Attention units are (row, kv head, context split); the last split to
-//     finish merges the partials in split order.
-//   * Between phases a grid barrier: each workgroup adds one to one of 64
-//     counters (one per 64-byte line) and polls all of them. Counters only
-//     grow; the host passes the barrier count of earlier launches, so targets
-//     need no reset.
-//   * Data that crosses workgroups (residual stream, q, K/V appends,
-//     activations, partials) is written and read with device-scope (sc1)
-//     accesses, coherent across the XCDs' L2s; a wave waits for its stores
-//     (s_waitcnt 0) before any arrival is counted.
-//   * Every wait is bounded: after ~2 s a workgroup records an error in the
-//     workspace and the whole grid exits; later launches exit at once until
-//     the host resets the workspace.
+// Dataflow instead of barriers
+//   * Every value one workgroup hands to another is a 64-bit word: a 32-bit
+//     payload and a 32-bit tag (launch number << 8 | layer), written with one
+//     device-scope (sc1) store, coherent across the XCDs' L2s. A consumer
+//     polls exactly the words it needs until their tags match; the producer
+//     never waits. Phases overlap: a workgroup starts the next phase as soon
+//     as its own inputs are there.
+//   * Before polling, each wave requests its first weight chunks of the
+//     phase (weights never depend on the inputs), and attention requests the
+//     K/V rows of earlier positions, so the wait overlaps HBM traffic.
+//   * The residual stream lives in registers: every workgroup keeps the whole
+//     fp32 vector (7 values per thread at hidden 3584) and adds the attention
+//     and MLP outputs itself, in the reference's order, before each RMSNorm.
+//   * GEMV phases: each workgroup takes whole row tiles (64 rows, one per
+//     lane), its 8 waves split the tile's K chunks and combine in LDS. When a
+//     matrix has too few tiles for the grid (down projection) every tile's K
+//     range is cut into pieces; piece 0's workgroup adds the others' tagged
+//     partials in piece order. The activation vector sits in LDS.
+//   * Attention units are (row, kv head, context split); the O phase merges
+//     the splits in split order while filling its activations.
+//   * Buffers are reused across layers; tags carry the layer, and every
+//     reader of a reused buffer produces data that the next writer of that
+//     buffer (a later layer) waits for, so no write overtakes a read. The
+//     attention / MLP outputs that every workgroup reads for its residual
+//     have one buffer per layer.
+//   * Every wait is bounded: after ~2 s the workgroup records an error in the
+//     workspace and the grid exits; later launches exit at once until the
+//     host resets the workspace.
 // All reductions run in a fixed order, so results do not depend on timing,
 // and a row's arithmetic does not depend on the other rows of the batch.
 #include <algorithm>
-#include <type_traits>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 
 #include "common.h"
@@ -51,49 +54,86 @@
 namespace lyk {
 namespace {
 
+typedef unsigned long long u64;
+
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kPieces = 4;       // row tiles one wave's range may touch
-constexpr int kBarLines = 64;    // barrier counters
-constexpr int kLineWords = 16;   // 64 bytes
-constexpr int kNormPer = 16;     // hidden_size <= kNormPer * kThreads
+constexpr int kPieces = 4;           // row tiles one wave's range may touch
+constexpr int kNormPer = 10;         // hidden_size <= kNormPer * kThreads
 constexpr int kMaxRows = 4;
-constexpr int kAttnMaxSplits = 32;   // context splits per (row, kv head)
-constexpr int kAttnSplitTokens = 512;
-constexpr int kHandoverChunks = 13;  // ~4 us of per-CU streaming
+constexpr int kAttnMaxSplits = 12;   // context splits per (row, kv head)
+constexpr int kAttnSplitTokens = 128;
+constexpr int kPass = 64;            // attention tokens per pass (one per lane)
+constexpr int kMinPieceChunks = 4;   // K chunks per piece of a split tile, at least
+constexpr int kMaxPieces = 8;        // pieces per split tile, at most
 constexpr uint64_t kSpinTicks = 200000000ull;  // s_memrealtime is 100 MHz: 2 s
-
-enum Phase { kQkv = 0, kOut = 1, kGateUp = 2, kDown = 3, kHead = 4 };
+constexpr size_t kMaxDynamicLds = 48 * 1024;
 
 struct StepArgs {
     lyk_step_model md;
     lyk_step_io io;
     int* err;
-    uint32_t* epoch;      // barriers completed by earlier launches
-    unsigned* bar;
-    unsigned* tile_cnt;   // per row tile of the current GEMV phase
-    float* part;          // [grid][2][M][64] GEMV partials
-    float* attn_ml;       // [rows*nkv][splits][G][2] per-split max and sum
-    float* attn_acc;      // [rows*nkv][splits][G][hd] per-split unnormalised output
-    float* h;             // [2][kMaxRows][hidden] residual entering a layer (by parity)
-    float* d_attn;        // [M][hidden] attention block output (O GEMV)
-    float* d_mlp;         // [M][hidden] MLP block output (down GEMV)
-    float* q;             // [M][nq*hd] rotated queries
-    uint16_t* act;        // [M][ld_act] fp16 SiLU(gate) * up
-    float* best_v;        // [M][head tiles] greedy candidates
-    int* best_i;
-    int* best_bad;
-    int ld_act;
-    int attn_split_tokens;  // context tokens per attention split, about
-    int attn_max_splits;    // splits per (row, kv head), at most
-    uint32_t barriers;      // grid barriers of one launch
+    uint32_t* seq;        // [grid] launches completed, per workgroup
+    u64* qkv;             // [M][(nq+2nkv)*hd] raw QKV sums (fp32 bits)
+    u64* attn_ml;         // [M][nkv][splits][G][2] per-split max and sum
+    u64* attn_acc;        // [M][nkv][splits][G][hd] per-split unnormalised output
+    u64* attn_out;        // [M][nq*hd] attention output
+    u64* d_attn;          // [layers][M][hidden] attention block output
+    u64* d_mlp;           // [layers][M][hidden] MLP block output
+    u64* act;             // [M][intermediate/2] fp16 pairs of SiLU(gate) * up
+    u64* dpart;           // [5][dpart_stride] split-tile partials [tiles][pieces][M][64] per GEMV kind
+    size_t dpart_stride;
+    u64* best;            // [M][head tiles][3] greedy candidates (value, index, non-finite)
+    int attn_split_tokens;  // context tokens per attention split, at least
+    int phases;             // phases of one launch (trace layout)
 };
 
 // ------------------------------------------------------------ primitives
 
 __device__ __forceinline__ void store_sc1_u16(uint16_t* p, uint16_t v) { store_sc1<uint16_t>(p, v); }
-__device__ __forceinline__ uint32_t load_sc1_u32(const uint32_t* p) { return load_sc1<uint32_t>(p); }
-__device__ __forceinline__ int load_sc1_i32(const int* p) { return load_sc1<int>(p); }
+
+__device__ __forceinline__ void put(u64* p, uint32_t payload, uint32_t tag) {
+    store_sc1<u64>(p, ((u64)tag << 32) | payload);
+}
+__device__ __forceinline__ bool take(const u64* p, uint32_t tag, uint32_t& payload) {
+    const u64 w = load_sc1<u64>(p);
+    payload = (uint32_t)w;
+    return (uint32_t)(w >> 32) == tag;
+}
+__device__ __forceinline__ uint32_t fbits(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ float bitsf(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+__device__ __forceinline__ bool aborted(const StepArgs& a) { return load_sc1<int>(a.err) != 0; }
+
+// Polls until `pending()` (which re-reads the words still missing and
+// returns how many remain) reaches 0. Bounded: records an error after ~2 s
+// and gives up when any workgroup has. Per thread; the caller combines the
+// result over the workgroup.
+template <class F>
+__device__ __forceinline__ bool spin(const StepArgs& a, F pending) {
+    if (pending() == 0) return true;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 1;; ++it) {
+        __builtin_amdgcn_s_sleep(2);
+        if (pending() == 0) return true;
+        if ((it & 15) == 0) {
+            if (aborted(a)) return false;
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
+                store_sc1(a.err, 1);
+                return false;
+            }
+        }
+    }
+}
+
+// threadIdx.x through an opaque move: values derived from it are recomputed
+// in every phase instead of being hoisted out of the layer loop and kept
+// live (in registers) across all phases.
+__device__ __forceinline__ int phase_tid() {
+    int t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+    return t;
+}
 
 // The layer table entry (device memory) as 13 pointer-sized loads.
 __device__ __forceinline__ lyk_step_layer load_layer(const lyk_step_layer* p) {
@@ -105,80 +145,12 @@ __device__ __forceinline__ lyk_step_layer load_layer(const lyk_step_layer* p) {
     return __builtin_bit_cast(lyk_step_layer, w);
 }
 
-// Profiling timestamp of workgroup 0 (lyk_step_io::trace): kind 0 = the
-// phase's inputs are ready (x window / queries and K/V loaded), kind 1 = its
-// main loop is done.
-__device__ __forceinline__ void mark(const StepArgs& a, int phase, int kind) {
-    if (a.io.trace && blockIdx.x == 0 && threadIdx.x == 0)
-        st(a.io.trace + (2 + kind) * a.barriers + 2 + phase, (uint64_t)__builtin_amdgcn_s_memrealtime());
-}
-
-__device__ __forceinline__ bool aborted(const StepArgs& a) { return load_sc1_i32(a.err) != 0; }
-
-// threadIdx.x through an opaque move: values derived from it are recomputed
-// in every phase instead of being hoisted out of the layer loop and kept
-// live (in registers) across all phases.
-__device__ __forceinline__ int phase_tid() {
-    int t;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
-    return t;
-}
-
-// Grid barrier number `idx` of this launch, in two halves so that loads
-// that do not depend on it can be issued in between. Arrival: every wave
-// waits for its own stores (s_waitcnt 0), then one count from the
-// workgroup. Wait: wave 0 polls all counters; false (for the whole
-// workgroup) when the grid is aborting.
-__device__ __forceinline__ void grid_arrive(const StepArgs& a, uint32_t idx) {
-    publish_sc1_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int G = gridDim.x;
-        const int lines = G < kBarLines ? G : kBarLines;
-        if (a.io.trace && blockIdx.x == 0)
-            st(a.io.trace + a.barriers + 2 + idx, (uint64_t)__builtin_amdgcn_s_memrealtime());
-        __hip_atomic_fetch_add(gp(a.bar + (blockIdx.x % lines) * kLineWords), 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
-__device__ __forceinline__ bool grid_wait(const StepArgs& a, uint32_t epoch, uint32_t idx) {
-    __shared__ int ok;
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        const int G = gridDim.x;
-        const int lines = G < kBarLines ? G : kBarLines;
-        const uint32_t gen = epoch + idx + 1;
-        const uint32_t per = lane < lines ? (uint32_t)((G - 1 - lane) / lines + 1) : 0u;
-        const uint32_t target = gen * per;
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        int good = 1;
-        while (true) {
-            bool done = true;
-            if (lane < lines) {
-                const uint32_t v = load_sc1_u32(a.bar + lane * kLineWords);
-                done = (int32_t)(v - target) >= 0;
-            }
-            if (__all(done)) break;
-            if (aborted(a)) { good = 0; break; }
-            if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
-                if (lane == 0) store_sc1(a.err, 1);
-                good = 0;
-                break;
-            }
-        }
-        if (lane == 0) {
-            ok = good;
-            if (a.io.trace && blockIdx.x == 0) st(a.io.trace + idx + 1, (uint64_t)__builtin_amdgcn_s_memrealtime());
-        }
-    }
-    __syncthreads();
-    return ok != 0;
-}
-
-__device__ __forceinline__ bool grid_sync(const StepArgs& a, uint32_t epoch, uint32_t idx) {
-    grid_arrive(a, idx);
-    return grid_wait(a, epoch, idx);
+// Profiling timestamp (lyk_step_io::trace) of this workgroup: phase ph
+// entered (0), inputs ready (1), main loop done (2), outputs written (3).
+__device__ __forceinline__ void mark(const StepArgs& a, int ph, int kind) {
+    if (a.io.trace && threadIdx.x == 0)
+        st(a.io.trace + (size_t)blockIdx.x * (2 + 4 * a.phases) + 2 + 4 * ph + kind,
+           (uint64_t)__builtin_amdgcn_s_memrealtime());
 }
 
 // Sum of v over the workgroup for M rows; every thread gets the sums. Waves
@@ -227,242 +199,56 @@ __device__ __forceinline__ Mat make_mat(const void* w, const void* s, int n, int
     return m;
 }
 
+template <bool Q8>
+constexpr int chunk_k() { return Q8 ? 128 : 256; }
+
+// Pieces each row tile's K range is cut into: 1 unless the matrix has too
+// few tiles to give every workgroup work and each piece keeps at least
+// kMinPieceChunks chunks.
+__host__ __device__ __forceinline__ int tile_pieces(int64_t tiles, int64_t chunks, int G) {
+    if (tiles * 2 > G) return 1;
+    int64_t p = G / tiles;
+    const int64_t pmax = chunks / kMinPieceChunks;
+    if (p > pmax) p = pmax;
+    if (p > kMaxPieces) p = kMaxPieces;
+    return p < 1 ? 1 : (int)p;
+}
+
 // The workgroup's share of a phase: chunk range [f0, f1) of the flattened
-// (tile, chunk) space and the window of K chunks it reads, as LDS slots
-// slot(c) = (c - ca) mod chunks < win.
+// (tile, chunk) space (whole tiles, or one piece of one tile) and the window
+// of K chunks it reads: LDS slot s holds chunk ca + s.
 struct Part {
-    int64_t U, f0, f1;
-    int gp;   // workgroups with work
+    int64_t f0, f1;
+    int pieces, gp;   // pieces per tile; workgroups with work
     int ca, win;
     bool busy;
 };
 
-// Whole row tiles per workgroup (no cross-workgroup sums) unless splitting
-// tiles along K saves more chunk-streaming time than the partial-sum hand
-// over costs (about kHandoverChunks chunks of streaming at the per-CU share
-// of HBM bandwidth).
-__host__ __device__ __forceinline__ bool tile_aligned(int64_t tiles, int64_t chunks, int G) {
-    const int64_t U = tiles * chunks;
-    return (tiles + G - 1) / G * chunks <= (U + G - 1) / G + kHandoverChunks;
-}
-
 __device__ __forceinline__ Part partition(const Mat& A) {
     Part p;
-    p.U = (int64_t)A.tiles * A.chunks;
-    const int G = gridDim.x;
-    const int b = blockIdx.x;
-    if (tile_aligned(A.tiles, A.chunks, G)) {
+    const int G = gridDim.x, b = blockIdx.x;
+    p.pieces = tile_pieces(A.tiles, A.chunks, G);
+    if (p.pieces == 1) {
         p.gp = A.tiles < G ? A.tiles : G;
         p.busy = b < p.gp;
         p.f0 = p.busy ? (int64_t)A.tiles * b / p.gp * A.chunks : 0;
         p.f1 = p.busy ? (int64_t)A.tiles * (b + 1) / p.gp * A.chunks : 0;
-    } else {
-        p.gp = (int)(p.U < G ? p.U : G);
-        p.busy = b < p.gp;
-        p.f0 = p.busy ? p.U * b / p.gp : 0;
-        p.f1 = p.busy ? p.U * (b + 1) / p.gp : 0;
-    }
-    const int64_t len = p.f1 - p.f0;
-    if (len >= A.chunks) {
         p.ca = 0;
         p.win = A.chunks;
     } else {
-        p.ca = (int)(p.f0 % A.chunks);
-        p.win = (int)len;
+        p.gp = A.tiles * p.pieces;
+        p.busy = b < p.gp;
+        const int t = b / p.pieces, s = b % p.pieces;
+        const int c0 = A.chunks * s / p.pieces, c1 = A.chunks * (s + 1) / p.pieces;
+        p.f0 = p.busy ? (int64_t)t * A.chunks + c0 : 0;
+        p.f1 = p.busy ? (int64_t)t * A.chunks + c1 : 0;
+        p.ca = c0;
+        p.win = c1 - c0;
     }
     return p;
 }
 
-// Workgroup holding flattened chunk f (every workgroup < gp has work).
-__device__ __forceinline__ int wg_of(int64_t f, const Part& p) {
-    return (int)(((f + 1) * p.gp + p.U - 1) / p.U - 1);
-}
-
-template <bool Q8>
-constexpr int chunk_k() { return Q8 ? 128 : 256; }
-
-// Residual stream of row m entering a norm: base (+ d1) (+ d2), added in
-// that order (the reference's h += attn; h += mlp). Every workgroup computes
-// the whole row for its RMSNorm; it also stores its own slice [H*b/G,
-// H*(b+1)/G) to `out` when given (the next layer's base).
-struct ResidualSrc {
-    const float* base;   // fp32 rows [M][H] (or embedding rows when embed)
-    const float* d1;
-    const float* d2;
-    float* out;
-    bool embed;          // base rows are embed[tokens[m]] (read-only, plain loads)
-};
-
-// x window <- RMSNorm(residual) (fp16), for the chunks of the window; zero
-// beyond k. Runs on every workgroup (idle ones only write their slice).
-template <int M, bool Q8>
-__device__ __forceinline__ void fill_norm(const StepArgs& a, const float* gamma, const ResidualSrc& r,
-                                          const Mat& A, const Part& p, uint16_t* xs, int tid) {
-    constexpr int CK = chunk_k<Q8>();
-    const int H = a.md.hidden_size;
-    const float* base[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-        base[m] = r.embed ? a.md.embed + (size_t)load_sc1(a.io.tokens + m) * H : r.base + (size_t)m * H;
-    float v[M][kNormPer];
-#pragma unroll
-    for (int j = 0; j < kNormPer; ++j) {
-        const int i = tid + j * kThreads;
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            float x = 0.0f;
-            if (i < H) {
-                x = r.embed ? ld(base[m] + i) : load_sc1(base[m] + i);
-                if (r.d1) x += load_sc1(r.d1 + (size_t)m * H + i);
-                if (r.d2) x += load_sc1(r.d2 + (size_t)m * H + i);
-            }
-            v[m][j] = x;
-        }
-    }
-    if (r.out) {
-        const int b = blockIdx.x, G = gridDim.x;
-        const int i0 = (int)((int64_t)H * b / G), i1 = (int)((int64_t)H * (b + 1) / G);
-#pragma unroll
-        for (int j = 0; j < kNormPer; ++j) {
-            const int i = tid + j * kThreads;
-            if (i >= i0 && i < i1)
-#pragma unroll
-                for (int m = 0; m < M; ++m) store_sc1(r.out + (size_t)m * H + i, v[m][j]);
-        }
-    }
-    if (!p.busy) return;
-    float ss[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kNormPer; ++j) s = fmaf(v[m][j], v[m][j], s);
-        ss[m] = s;
-    }
-    block_sum_rows<M>(ss, tid);
-    float scale[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) scale[m] = 1.0f / sqrtf(ss[m] / (float)H + a.md.rms_norm_eps);
-#pragma unroll
-    for (int j = 0; j < kNormPer; ++j) {
-        const int i = tid + j * kThreads;
-        if (i < H) {
-            const int c = i / CK;
-            const int slot = (c - p.ca + A.chunks) % A.chunks;
-            if (slot < p.win) {
-                const float g = ld(gamma + i);
-#pragma unroll
-                for (int m = 0; m < M; ++m)
-                    xs[((size_t)m * p.win + slot) * CK + (i % CK)] = f2h(v[m][j] * scale[m] * g);
-            }
-        }
-    }
-    // zero the window past k
-    const int kp = A.chunks * CK;
-    for (int i = H + tid; i < kp; i += kThreads) {
-        const int c = i / CK;
-        const int slot = (c - p.ca + A.chunks) % A.chunks;
-        if (slot < p.win)
-#pragma unroll
-            for (int m = 0; m < M; ++m) xs[((size_t)m * p.win + slot) * CK + (i % CK)] = 0;
-    }
-}
-
-// x window <- fp16 rows src[m*ld ...] (zero-padded to chunks*CK by the
-// caller's buffer layout).
-template <int M, bool Q8>
-__device__ __forceinline__ void fill_copy(const uint16_t* src, int ld, const Mat& A, const Part& p,
-                                          uint16_t* xs, int tid) {
-    constexpr int CK = chunk_k<Q8>();
-    constexpr int W = CK / 2;  // dwords per chunk row
-    if (!p.busy) return;
-    const int total = M * p.win * W;
-    uint32_t* dst = reinterpret_cast<uint32_t*>(xs);
-    for (int e0 = tid; e0 < total; e0 += kThreads * 8) {
-        uint32_t v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int e = e0 + u * kThreads;
-            v[u] = 0;
-            if (e < total) {
-                const int m = e / (p.win * W), r = e % (p.win * W);
-                const int slot = r / W, w = r % W;
-                const int c = (p.ca + slot) % A.chunks;
-                v[u] = load_sc1_u32(reinterpret_cast<const uint32_t*>(src + (size_t)m * ld + (size_t)c * CK) + w);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int e = e0 + u * kThreads;
-            if (e < total) dst[e] = v[u];
-        }
-    }
-}
-
-// Context split of a row: splits of about split_tokens tokens, at most
-// max_splits; a row's arithmetic depends only on its own context length.
-__device__ __forceinline__ int attn_splits(int ctx, int split_tokens, int max_splits) {
-    const int s = (ctx + split_tokens - 1) / split_tokens;
-    return s < 1 ? 1 : (s > max_splits ? max_splits : s);
-}
-
-// x window <- the attention output: the fixed-order merge of the context
-// splits' partials (max, sum, unnormalised output per head) written by the
-// attention phase, out = sum_s e_s acc_s / sum_s e_s l_s with
-// e_s = exp(m_s - max_s m_s).
-template <int M, bool Q8>
-__device__ __forceinline__ void fill_attn(const StepArgs& a, const Mat& A, const Part& p, uint16_t* xs,
-                                          int tid) {
-    constexpr int CK = chunk_k<Q8>();
-    if (!p.busy) return;
-    const int nq = a.md.num_heads, nkv = a.md.num_kv_heads, hd = a.md.head_dim, G = nq / nkv;
-    const int MS = a.attn_max_splits;
-    // heads of the window: consecutive (mod nq) from the head of chunk ca
-    const int h0 = p.ca * CK / hd;
-    const int nh = min(nq, (p.win * CK + hd - 1) / hd + 1);
-    // per (row, window head): e_s = exp(m_s - max) for each split, then L
-    float* wts = reinterpret_cast<float*>(xs + (size_t)M * p.win * CK);  // [M][nh][MS + 1]
-    for (int e = tid; e < M * nh; e += kThreads) {
-        const int m = e / nh, hw = e % nh;
-        const int hq = (h0 + hw) % nq;
-        const int S = attn_splits(load_sc1(a.io.positions + m) + 1, a.attn_split_tokens, MS);
-        const size_t grp = (size_t)m * nkv + hq / G;
-        const int h = hq % G;
-        float* w = wts + (size_t)e * (MS + 1);
-        float mx = -INFINITY;
-        for (int s = 0; s < S; ++s) mx = fmaxf(mx, load_sc1(&a.attn_ml[((grp * MS + s) * G + h) * 2]));
-        float L = 0.0f;
-        for (int s = 0; s < S; ++s) {
-            const float* ml = &a.attn_ml[((grp * MS + s) * G + h) * 2];
-            const float es = expf(load_sc1(ml) - mx);
-            w[s] = es;
-            L += load_sc1(ml + 1) * es;
-        }
-        w[MS] = L;
-    }
-    __syncthreads();
-    const int kq = nq * hd;
-    for (int e = tid; e < M * p.win * CK; e += kThreads) {
-        const int m = e / (p.win * CK), r = e % (p.win * CK);
-        const int slot = r / CK, i = r % CK;
-        const int k = ((p.ca + slot) % A.chunks) * CK + i;
-        float out = 0.0f;
-        if (k < kq) {
-            const int hq = k / hd, d = k % hd;
-            const int hw = (hq - h0 + nq) % nq;
-            const int S = attn_splits(load_sc1(a.io.positions + m) + 1, a.attn_split_tokens, MS);
-            const size_t grp = (size_t)m * nkv + hq / G;
-            const int h = hq % G;
-            const float* w = wts + ((size_t)m * nh + hw) * (MS + 1);
-            float o = 0.0f;
-            for (int s = 0; s < S; ++s) o += load_sc1(&a.attn_acc[((grp * MS + s) * G + h) * (size_t)hd + d]) * w[s];
-            out = o / w[MS];
-        }
-        xs[((size_t)m * p.win + slot) * CK + i] = f2h(out);
-    }
-}
-
-// Accumulates chunk f of the matrix into acc (x from the LDS window).
+// Accumulates one chunk of the matrix into acc (x from the LDS window).
 template <int M, bool Q8>
 struct ChunkMath;
 
@@ -479,45 +265,38 @@ struct ChunkMath<M, false> {
         s4 = __builtin_nontemporal_load(gp(static_cast<const u32x4*>(A.s) + (size_t)f * 64 + lane));
         __builtin_amdgcn_sched_barrier(0);
     }
-    __device__ __forceinline__ static void compute(const u32x4 (&w)[8], const u32x4& s4, const uint16_t* xs,
-                                                   int xstride, float (&acc)[M], uint32_t vmagic) {
+    // One group (32 codes) against x[32]: four independent dot2 chains.
+    __device__ __forceinline__ static float group(const u32x4& w, const u32x4* xv, uint32_t vmagic) {
         const half2_t off_a = {(half_t)-1032.0f, (half_t)-1032.0f};
         const half2_t off_b = {(half_t)-1152.0f, (half_t)-1152.0f};
-        float gs[M][8];
+        const uint32_t u4[4] = {w.x, w.y, w.z, w.w};
+        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t u4[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
-            half2_t qa[8], qb[8];
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t u = u4[d], t = u >> 8;
+            const u32x4 xx = xv[d];
+            a0 = dot2(as_half2((u & 0x000F000Fu) | vmagic) + off_a, as_half2(xx.x), a0);
+            b0 = dot2(as_half2((u & 0x00F000F0u) | vmagic) + off_b, as_half2(xx.y), b0);
+            a1 = dot2(as_half2((t & 0x000F000Fu) | vmagic) + off_a, as_half2(xx.z), a1);
+            b1 = dot2(as_half2((t & 0x00F000F0u) | vmagic) + off_b, as_half2(xx.w), b1);
+        }
+        return (b0 + b1) * 0.0625f + (a0 + a1);
+    }
+    __device__ __forceinline__ static void compute(const u32x4 (&w)[8], const u32x4& s4, const uint16_t* xs,
+                                                   int xstride, float (&acc)[M], uint32_t vmagic) {
+        const uint32_t sw[4] = {s4.x, s4.y, s4.z, s4.w};
+        // groups in pairs: two groups' math interleaves, x of one pair at a time
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const uint32_t u = u4[d], t = u >> 8;
-                qa[2 * d] = as_half2((u & 0x000F000Fu) | vmagic) + off_a;
-                qb[2 * d] = as_half2((u & 0x00F000F0u) | vmagic) + off_b;
-                qa[2 * d + 1] = as_half2((t & 0x000F000Fu) | vmagic) + off_a;
-                qb[2 * d + 1] = as_half2((t & 0x00F000F0u) | vmagic) + off_b;
-            }
+        for (int j = 0; j < 8; j += 2) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const u32x4* xv = reinterpret_cast<const u32x4*>(xs + (size_t)m * xstride + j * 32);
-                float a = 0.0f, b = 0.0f;
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const u32x4 xx = xv[d];
-                    a = dot2(qa[2 * d], as_half2(xx.x), a);
-                    b = dot2(qb[2 * d], as_half2(xx.y), b);
-                    a = dot2(qa[2 * d + 1], as_half2(xx.z), a);
-                    b = dot2(qb[2 * d + 1], as_half2(xx.w), b);
-                }
-                gs[m][j] = b * 0.0625f + a;
+                const u32x4* x0 = reinterpret_cast<const u32x4*>(xs + (size_t)m * xstride + j * 32);
+                const float g0 = group(w[j], x0, vmagic);
+                const float g1 = group(w[j + 1], x0 + 4, vmagic);
+                acc[m] = fmaf(g0, h2f(uint16_t(sw[j >> 1])), acc[m]);
+                acc[m] = fmaf(g1, h2f(uint16_t(sw[j >> 1] >> 16)), acc[m]);
             }
-            __builtin_amdgcn_sched_barrier(0);  // x reads of one group at a time
-        }
-        const uint32_t sw[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float s = h2f(uint16_t(sw[j >> 1] >> (16 * (j & 1))));
-#pragma unroll
-            for (int m = 0; m < M; ++m) acc[m] = fmaf(gs[m][j], s, acc[m]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 };
@@ -534,71 +313,289 @@ struct ChunkMath<M, true> {
         }
         (void)s4;
     }
+    __device__ __forceinline__ static float block(const u32x4& w, const u32x4* xv) {
+        const half2_t off = {(half_t)-1152.0f, (half_t)-1152.0f};
+        const uint32_t u4[4] = {w.x, w.y, w.z, w.w};
+        const u32x4 x0 = xv[0], x1 = xv[1];
+        const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            a0 = dot2(as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04010400u)) + off, as_half2(xw[2 * d]), a0);
+            a1 = dot2(as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04030402u)) + off, as_half2(xw[2 * d + 1]), a1);
+        }
+        return a0 + a1;
+    }
     __device__ __forceinline__ static void compute(const u32x4 (&w)[8], const u32x4&, const uint16_t* xs,
                                                    int xstride, float (&acc)[M], uint32_t) {
-        const half2_t off = {(half_t)-1152.0f, (half_t)-1152.0f};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t u4[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
-            half2_t q[8];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                q[2 * d] = as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04010400u)) + off;
-                q[2 * d + 1] = as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04030402u)) + off;
-            }
+        for (int j = 0; j < 8; j += 2) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const u32x4* xv = reinterpret_cast<const u32x4*>(xs + (size_t)m * xstride + j * 16);
-                const u32x4 x0 = xv[0], x1 = xv[1];
-                float a = acc[m];
-                a = dot2(q[0], as_half2(x0.x), a);
-                a = dot2(q[1], as_half2(x0.y), a);
-                a = dot2(q[2], as_half2(x0.z), a);
-                a = dot2(q[3], as_half2(x0.w), a);
-                a = dot2(q[4], as_half2(x1.x), a);
-                a = dot2(q[5], as_half2(x1.y), a);
-                a = dot2(q[6], as_half2(x1.z), a);
-                a = dot2(q[7], as_half2(x1.w), a);
-                acc[m] = a;
+                const u32x4* x0 = reinterpret_cast<const u32x4*>(xs + (size_t)m * xstride + j * 16);
+                const float g0 = block(w[j], x0);
+                const float g1 = block(w[j + 1], x0 + 2);
+                acc[m] += g0;
+                acc[m] += g1;
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
 };
 
-// Runs the workgroup's share of one GEMV phase. The wave's first two chunks
-// of weights are requested before the grid barrier that publishes the
-// phase's inputs (weights never depend on them), so the barrier and the
-// input fill overlap the first HBM round trip. `fill` writes the x window;
-// `epi(tile, v, lane)` finishes a tile (v = the tile's 64 row sums of each
-// batch row, one row per lane; called by one whole wave). bar < 0: no
-// barrier before the phase. Returns false when the grid is aborting.
-template <int M, bool Q8, class Fill, class Epi>
-__device__ __forceinline__ bool gemv_phase(const StepArgs& a, uint32_t epoch, int bar, const Mat& A, Fill fill,
-                                           Epi epi) {
+// ------------------------------------------------------------ phase inputs
+
+// Residual rows (registers, element i = tid + j*kThreads of each row) plus
+// the tagged block output d[m*H + i] of this layer, polled.
+template <int M>
+__device__ __forceinline__ bool residual_add(const StepArgs& a, float (&h)[M][kNormPer], const u64* d,
+                                             uint32_t tag, int tid) {
+    const int H = a.md.hidden_size;
+    uint32_t have[M];   // bit j: element j of row m received
+#pragma unroll
+    for (int m = 0; m < M; ++m) have[m] = 0;
+    float add[M][kNormPer];
+    auto pending = [&]() {
+        int missing = 0;
+#pragma unroll
+        for (int j = 0; j < kNormPer; ++j) {
+            const int i = tid + j * kThreads;
+            if (i >= H) continue;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if (have[m] >> j & 1) continue;
+                uint32_t u;
+                if (take(d + (size_t)m * H + i, tag, u)) {
+                    add[m][j] = bitsf(u);
+                    have[m] |= 1u << j;
+                } else {
+                    ++missing;
+                }
+            }
+        }
+        return missing;
+    };
+    if (!spin(a, pending)) return false;
+#pragma unroll
+    for (int j = 0; j < kNormPer; ++j)
+        if (tid + j * kThreads < H)
+#pragma unroll
+            for (int m = 0; m < M; ++m) h[m][j] += add[m][j];
+    return true;
+}
+
+// x window <- fp16 RMSNorm(h) * gamma over the chunks of the window, zero
+// beyond k (the reference order: h * (1/sqrt(mean(h^2) + eps)) * gamma).
+template <int M, bool Q8>
+__device__ __forceinline__ void norm_window(const StepArgs& a, const float (&h)[M][kNormPer], const float* gamma,
+                                            const Mat& A, const Part& p, uint16_t* xs, int tid) {
+    constexpr int CK = chunk_k<Q8>();
+    const int H = a.md.hidden_size;
+    float ss[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kNormPer; ++j) s = fmaf(h[m][j], h[m][j], s);   // zero past H
+        ss[m] = s;
+    }
+    block_sum_rows<M>(ss, tid);
+    float scale[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) scale[m] = 1.0f / sqrtf(ss[m] / (float)H + a.md.rms_norm_eps);
+#pragma unroll
+    for (int j = 0; j < kNormPer; ++j) {
+        const int i = tid + j * kThreads;
+        if (i < H) {
+            const int slot = i / CK - p.ca;
+            if (slot >= 0 && slot < p.win) {
+                const float g = ld(gamma + i);
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+                    xs[((size_t)m * p.win + slot) * CK + (i % CK)] = f2h(h[m][j] * scale[m] * g);
+            }
+        }
+    }
+    const int kp = (p.ca + p.win) * CK;
+    for (int i = (H > p.ca * CK ? H : p.ca * CK) + tid; i < kp; i += kThreads) {
+        const int slot = i / CK - p.ca;
+#pragma unroll
+        for (int m = 0; m < M; ++m) xs[((size_t)m * p.win + slot) * CK + (i % CK)] = 0;
+    }
+}
+
+// x window <- fp16 of the tagged fp32 attention outputs [M][nq*hd] of the
+// window's chunks.
+template <int M, bool Q8>
+__device__ __forceinline__ bool fill_attn(const StepArgs& a, uint32_t tag, const Mat& A, const Part& p,
+                                          uint16_t* xs, int tid) {
+    constexpr int CK = chunk_k<Q8>();
+    if (!p.busy) return true;
+    const int kq = a.md.num_heads * a.md.head_dim;
+    const int total = M * p.win * CK;
+    bool ok = true;
+    for (int e0 = tid; e0 < total; e0 += kThreads * 8) {
+        uint32_t v[8];
+        uint32_t have = 0;
+        auto pending = [&]() {
+            int missing = 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int e = e0 + u * kThreads;
+                if (e >= total || (have >> u & 1)) continue;
+                const int m = e / (p.win * CK), k = p.ca * CK + e % (p.win * CK);
+                if (k >= kq) {
+                    v[u] = 0;
+                    have |= 1u << u;
+                    continue;
+                }
+                if (take(a.attn_out + (size_t)m * kq + k, tag, v[u])) have |= 1u << u;
+                else ++missing;
+            }
+            return missing;
+        };
+        ok = spin(a, pending) && ok;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u * kThreads;
+            if (e < total) xs[e] = f2h(bitsf(v[u]));
+        }
+    }
+    return ok;
+}
+
+// x window <- the tagged SiLU(gate) * up pairs of the window's chunks.
+template <int M, bool Q8>
+__device__ __forceinline__ bool fill_act(const StepArgs& a, uint32_t tag, const Mat& A, const Part& p,
+                                         uint16_t* xs, int tid) {
+    constexpr int CK = chunk_k<Q8>();
+    constexpr int W = CK / 2;  // pairs per chunk row
+    if (!p.busy) return true;
+    const int In2 = a.md.intermediate_size / 2;
+    const int total = M * p.win * W;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(xs);
+    bool ok = true;
+    for (int e0 = tid; e0 < total; e0 += kThreads * 8) {
+        uint32_t v[8];
+        uint32_t have = 0;
+        auto pending = [&]() {
+            int missing = 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int e = e0 + u * kThreads;
+                if (e >= total || (have >> u & 1)) continue;
+                const int m = e / (p.win * W), r = e % (p.win * W);
+                const int pi = p.ca * W + r;   // pair index
+                if (pi >= In2) {
+                    v[u] = 0;
+                    have |= 1u << u;
+                    continue;
+                }
+                if (take(a.act + (size_t)m * In2 + pi, tag, v[u])) have |= 1u << u;
+                else ++missing;
+            }
+            return missing;
+        };
+        ok = spin(a, pending) && ok;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = e0 + u * kThreads;
+            if (e < total) dst[e] = v[u];
+        }
+    }
+    return ok;
+}
+
+struct Best {
+    float v;
+    int i;
+};
+__device__ __forceinline__ Best better(Best x, Best y) {
+    if (y.v > x.v || (y.v == x.v && y.i < x.i)) return y;
+    return x;
+}
+
+enum Kind { kQkv = 0, kAttn = 1, kOut = 2, kGateUp = 3, kDown = 4, kHead = 5 };
+
+// Runs the workgroup's share of one GEMV phase of the given kind. The wave's
+// first two chunks are requested first; then the phase's inputs are polled
+// into the x window (every workgroup takes part in the residual updates, so
+// idle ones keep theirs current); then the stream. A tile cut into K pieces
+// is finished by piece 0's workgroup, which adds the others' tagged partials
+// in piece order. Returns false when the grid is aborting.
+template <int M, bool Q8>
+__device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, int l, const lyk_step_layer& Lw,
+                                          float (&h)[M][kNormPer], uint32_t tag0) {
     const int tid = phase_tid();
     using CM = ChunkMath<M, Q8>;
     constexpr int CK = CM::CK;
     extern __shared__ __align__(16) unsigned char smem[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
     float* red = reinterpret_cast<float*>(smem);  // aliases xs after the stream
+    const int H = a.md.hidden_size, nq = a.md.num_heads, nkv = a.md.num_kv_heads, hd = a.md.head_dim;
+    const int In = a.md.intermediate_size, L = a.md.num_layers, V = a.md.vocab_size;
+    const int rows = (nq + 2 * nkv) * hd;
+    const uint32_t tag = tag0 | (uint32_t)l;   // l == L for the LM head
+    const void* wp;
+    const void* sp;
+    int n, k;
+    switch (kind) {
+        case kQkv: wp = Lw.qkv_w; sp = Lw.qkv_s; n = rows; k = H; break;
+        case kOut: wp = Lw.o_w; sp = Lw.o_s; n = H; k = nq * hd; break;
+        case kGateUp: wp = Lw.gateup_w; sp = Lw.gateup_s; n = In; k = H; break;
+        case kDown: wp = Lw.down_w; sp = Lw.down_s; n = H; k = In; break;
+        default: wp = a.md.lm_head_w; sp = a.md.lm_head_s; n = V; k = H; break;
+    }
+    const Mat A = make_mat<Q8>(wp, sp, n, k, kind == kGateUp);
+    mark(a, ph, 0);
     const Part p = partition(A);
     const int b = blockIdx.x;
     const int lane = tid & 63, wave = uniform(tid >> 6);
     const int64_t len = p.f1 - p.f0;
     const int64_t w0 = p.f0 + len * wave / kWaves, w1 = p.f0 + len * (wave + 1) / kWaves;
 
-    if (bar >= 0) grid_arrive(a, (uint32_t)bar);
     u32x4 wa[8], wb[8], sa, sb;
     if (w0 < w1) CM::load(A, w0, lane, wa, sa);
     if (w0 + 1 < w1) CM::load(A, w0 + 1, lane, wb, sb);
-    if (bar >= 0 && !grid_wait(a, epoch, (uint32_t)bar)) return false;
 
-    fill(A, p, xs, tid);
-    if (!p.busy) return true;
-    __syncthreads();
-    mark(a, bar < 0 ? 0 : bar, 0);
+    // ---- inputs
+    bool ok = true;
+    if (kind == kQkv || kind == kGateUp || kind == kHead) {
+        // residual += the block output this norm follows, then RMSNorm
+        const u64* d = nullptr;
+        uint32_t dtag = 0;
+        const float* gamma;
+        if (kind == kQkv) {
+            if (l > 0) {
+                d = a.d_mlp + (size_t)(l - 1) * kMaxRows * H;
+                dtag = tag - 1;
+            }
+            gamma = Lw.input_norm;
+        } else if (kind == kGateUp) {
+            d = a.d_attn + (size_t)l * kMaxRows * H;
+            dtag = tag;
+            gamma = Lw.post_norm;
+        } else {
+            d = a.d_mlp + (size_t)(L - 1) * kMaxRows * H;
+            dtag = tag - 1;
+            gamma = a.md.final_norm;
+        }
+        if (d) ok = residual_add<M>(a, h, d, dtag, tid);
+        if (ok && p.busy) norm_window<M, Q8>(a, h, gamma, A, p, xs, tid);
+    } else if (kind == kOut) {
+        ok = fill_attn<M, Q8>(a, tag, A, p, xs, tid);
+    } else {
+        ok = fill_act<M, Q8>(a, tag, A, p, xs, tid);
+    }
+    if (__syncthreads_or(!ok)) return false;
+    mark(a, ph, 1);
+    if (!p.busy) {
+        mark(a, ph, 2);
+        mark(a, ph, 3);
+        return true;
+    }
 
+    // ---- stream
     const int xstride = p.win * CK;
     float accq[kPieces][M];
 #pragma unroll
@@ -620,13 +617,13 @@ __device__ __forceinline__ bool gemv_phase(const StepArgs& a, uint32_t epoch, in
         // int8 per-row scale of the current tile
         float srow = 1.0f;
         if constexpr (Q8) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
+        const int cend = p.pieces == 1 ? A.chunks : (int)(p.f1 - (int64_t)t * A.chunks);
         // One chunk: math on the buffer, then request the chunk two ahead
         // into it; a tile's sums go to its piece slot when the tile ends.
         auto step = [&](u32x4 (&wc)[8], u32x4& sc) -> bool {
-            const int slot = (c - p.ca + A.chunks) % A.chunks;
-            CM::compute(wc, sc, xs + (size_t)slot * CK, xstride, acc, vmagic);
+            CM::compute(wc, sc, xs + (size_t)(c - p.ca) * CK, xstride, acc, vmagic);
             const bool end = f + 1 == w1;
-            if (c + 1 == A.chunks || end) {
+            if (c + 1 == cend || c + 1 == A.chunks || end) {
 #pragma unroll
                 for (int qq = 0; qq < kPieces; ++qq)
                     if (qq == q)
@@ -652,7 +649,7 @@ __device__ __forceinline__ bool gemv_phase(const StepArgs& a, uint32_t epoch, in
         }
     }
     __syncthreads();  // every wave is done with the x window
-    mark(a, bar < 0 ? 0 : bar, 1);
+    mark(a, ph, 2);
     {
         const int64_t tf = w0 < w1 ? w0 / A.chunks : 0;
         const int np = w0 < w1 ? (int)((w1 - 1) / A.chunks - tf + 1) : 0;
@@ -664,7 +661,12 @@ __device__ __forceinline__ bool gemv_phase(const StepArgs& a, uint32_t epoch, in
     }
     __syncthreads();
 
+    // ---- finish the workgroup's tiles, one wave per tile
     const int tA = (int)(p.f0 / A.chunks), tB = (int)((p.f1 - 1) / A.chunks);
+    const bool greedy = a.io.mode == LYK_STEP_GREEDY;
+    // a region per GEMV kind: the kinds of one layer share tags
+    u64* dpart = a.dpart + (size_t)(kind == kQkv ? 0 : kind - 1) * a.dpart_stride;
+    bool good = true;
     for (int t = tA + wave; t <= tB; t += kWaves) {
         float v[M];
 #pragma unroll
@@ -677,249 +679,120 @@ __device__ __forceinline__ bool gemv_phase(const StepArgs& a, uint32_t epoch, in
 #pragma unroll
             for (int m = 0; m < M; ++m) v[m] += red[((w * kPieces + (t - tf)) * M + m) * 64 + lane];
         }
-        const bool full = p.f0 <= (int64_t)t * A.chunks && (int64_t)(t + 1) * A.chunks <= p.f1;
-        if (!full) {
-            const int slot = t == tA ? 0 : 1;
+        if (p.pieces > 1) {
+            const int np = p.pieces, s = b % np;
+            if (s > 0) {
 #pragma unroll
-            for (int m = 0; m < M; ++m)
-                store_sc1(&a.part[(((size_t)b * 2 + slot) * M + m) * 64 + lane], v[m]);
-            const int bf = wg_of((int64_t)t * A.chunks, p);
-            const int bl = wg_of((int64_t)(t + 1) * A.chunks - 1, p);
-            if (!arrive_last(&a.tile_cnt[t], (unsigned)(bl - bf + 1))) continue;
-#pragma unroll
-            for (int m = 0; m < M; ++m) v[m] = 0.0f;
-            for (int bb = bf; bb <= bl; ++bb) {
-                const int64_t fb = p.U * bb / p.gp;
-                const int sb = fb / A.chunks == t ? 0 : 1;
-#pragma unroll
-                for (int m = 0; m < M; ++m) v[m] += load_sc1(&a.part[(((size_t)bb * 2 + sb) * M + m) * 64 + lane]);
+                for (int m = 0; m < M; ++m)
+                    put(dpart + (((size_t)t * np + s) * M + m) * 64 + lane, fbits(v[m]), tag);
+                continue;
             }
-            if (lane == 0) store_sc1(&a.tile_cnt[t], 0u);
+            float got[kMaxPieces][M];
+            uint32_t have = 0;
+            auto pending = [&]() {
+                int missing = 0;
+#pragma unroll
+                for (int s2 = 1; s2 < kMaxPieces; ++s2) {
+                    if (s2 >= np) continue;
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const int bit = s2 * M + m;
+                        if (have >> bit & 1) continue;
+                        uint32_t u;
+                        if (take(dpart + (((size_t)t * np + s2) * M + m) * 64 + lane, tag, u)) {
+                            got[s2][m] = bitsf(u);
+                            have |= 1u << bit;
+                        } else {
+                            ++missing;
+                        }
+                    }
+                }
+                return missing;
+            };
+            if (!spin(a, pending)) {
+                good = false;
+                continue;
+            }
+#pragma unroll
+            for (int s2 = 1; s2 < kMaxPieces; ++s2)
+                if (s2 < np)
+#pragma unroll
+                    for (int m = 0; m < M; ++m) v[m] += got[s2][m];
         }
-        epi(t, v, lane);
+        const int r = t * 64 + lane;
+        switch (kind) {
+            case kQkv:
+                if (r < rows)
+#pragma unroll
+                    for (int m = 0; m < M; ++m) put(a.qkv + (size_t)m * rows + r, fbits(v[m]), tag);
+                break;
+            case kOut:
+            case kDown: {
+                u64* dst = (kind == kOut ? a.d_attn : a.d_mlp) + (size_t)l * kMaxRows * H;
+                if (r < H)
+#pragma unroll
+                    for (int m = 0; m < M; ++m) put(dst + (size_t)m * H + r, fbits(v[m]), tag);
+                break;
+            }
+            case kGateUp: {
+                // lanes 0-31 gate rows 32t.., lanes 32-63 the up rows; pairs
+                // of neighbouring rows go out as one word
+                const int j = t * 32 + lane;
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float up = __shfl_down(v[m], 32, 64);
+                    const float g = v[m];
+                    const uint32_t act = f2h(g / (1.0f + expf(-g)) * up);
+                    const uint32_t next = __shfl_down(act, 1, 64);
+                    if (lane < 32 && (lane & 1) == 0 && j < In)
+                        put(a.act + (size_t)m * (In / 2) + j / 2, act | (next << 16), tag);
+                }
+                break;
+            }
+            default: {
+                // LM head: logits, and each tile's greedy candidate (first
+                // index of the maximum, NaN never wins) and non-finite count
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    if (r < V) st(a.io.logits + (size_t)m * a.io.ld_logits + r, v[m]);
+                    if (!greedy) continue;
+                    float x = v[m];
+                    int bad = 0;
+                    if (r < V && !isfinite(x)) {
+                        bad = 1;
+                        if (isnan(x)) x = -INFINITY;
+                    }
+                    Best bst = r < V ? Best{x, r} : Best{-INFINITY, 0x7fffffff};
+#pragma unroll
+                    for (int o = 32; o > 0; o >>= 1)
+                        bst = better(bst, Best{__shfl_xor(bst.v, o, 64), __shfl_xor(bst.i, o, 64)});
+                    bad = (int)wave_sum((float)bad);
+                    if (lane == 0) {
+                        u64* w = a.best + ((size_t)m * A.tiles + t) * 3;
+                        put(w, fbits(bst.v), tag);
+                        put(w + 1, (uint32_t)bst.i, tag);
+                        put(w + 2, (uint32_t)bad, tag);
+                    }
+                }
+                break;
+            }
+        }
     }
+    if (__syncthreads_or(!good)) return false;
+    mark(a, ph, 3);
     return true;
 }
 
 // ------------------------------------------------------------ attention
 
-// One attention unit per (row, kv head, context split): the G query heads of
-// the group share every K/V element it loads. Tokens go in passes of P:
-// lane (token tl, dim slice dl) holds VEC dims of K and V of its token; the
-// next pass's K/V are requested before the current one is computed. Scores
-// reduce over the LPT lanes of a token, softmax runs online per head (wave
-// per head), and the unit writes (max, sum, unnormalised output) per head;
-// the O phase merges the splits.
-template <int M, int HD>
-__device__ __forceinline__ bool attention_phase(const StepArgs& a, uint32_t epoch, int bar,
-                                                const lyk_step_layer& Lw) {
-    const int tid = phase_tid();
-    constexpr int VEC = HD % 8 == 0 ? 8 : 2;       // halves of K/V per lane
-    constexpr int LPT = HD / VEC;                  // lanes per token
-    constexpr int TPW = 64 / LPT;                  // tokens per wave per round
-    constexpr int R = kWaves * TPW;                // tokens per round
-    constexpr int kRounds = R >= 64 ? 1 : 64 / R;
-    constexpr int P = R * kRounds;                 // tokens per pass
-    constexpr int kMaxG = 64 / VEC < 16 ? 64 / VEC : 16;
-    static_assert(64 % LPT == 0, "head dim must split evenly over lanes");
-    using KV = typename std::conditional<VEC == 8, u32x4, uint32_t>::type;
-    extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ float m_s[16], l_s[16], a_s[16];
-    const int nq = a.md.num_heads, nkv = a.md.num_kv_heads;
-    constexpr int hd = HD;
-    const int G = nq / nkv, bt = a.md.block_tokens;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int dl = lane % LPT, tl = lane / LPT;
-    const float scale = 1.0f / sqrtf((float)hd);
-    float* q_s = reinterpret_cast<float*>(smem);   // [G][hd]
-    float* p_s = q_s + G * hd;                     // [G][P]
-    float* o_s = reinterpret_cast<float*>(smem);   // [kWaves][G*hd] (after the passes)
-    const int MS = a.attn_max_splits;
-
-    if (!grid_sync(a, epoch, (uint32_t)bar)) return false;
-
-    int splits[M], ctxs[M], units = 0;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        ctxs[m] = load_sc1(a.io.positions + m) + 1;
-        splits[m] = attn_splits(ctxs[m], a.attn_split_tokens, MS);
-        units += nkv * splits[m];
-    }
-    for (int u = blockIdx.x; u < units; u += gridDim.x) {
-        int m = 0, r = u, S = splits[0], ctx = ctxs[0];
-#pragma unroll
-        for (int mm = 1; mm < M; ++mm)
-            if (m == mm - 1 && r >= nkv * S) {
-                r -= nkv * S;
-                m = mm;
-                S = splits[mm];
-                ctx = ctxs[mm];
-            }
-        const int g = r / S, s = r % S;
-        const int per = (ctx + S - 1) / S;
-        const int t0 = s * per, t1 = min(ctx, t0 + per);
-        const int* tab = a.io.block_tables + (size_t)m * a.io.table_stride;
-        const size_t head_stride = (size_t)bt * hd;   // one kv head of a block
-        const size_t blk_stride = (size_t)nkv * head_stride;
-        const uint16_t* kc = Lw.k_cache + (size_t)g * head_stride + dl * VEC;
-        const uint16_t* vc = Lw.v_cache + (size_t)g * head_stride + dl * VEC;
-
-        // K/V of this lane's tokens of the pass starting at c0. Rows before
-        // this step's position were written by earlier launches; the row at
-        // the position was written with device-scope stores earlier in this
-        // launch, before any read of its cache lines.
-        auto load_kv = [&](int c0, KV (&kk)[kRounds], KV (&vv)[kRounds]) {
-#pragma unroll
-            for (int rr = 0; rr < kRounds; ++rr) {
-                {
-                    const int t = c0 + rr * R + wave * TPW + tl;
-                    if (t < t1) {
-                        const size_t off = (size_t)ld(tab + t / bt) * blk_stride + (size_t)(t % bt) * hd;
-                        kk[rr] = ld(reinterpret_cast<const KV*>(kc + off));
-                        vv[rr] = ld(reinterpret_cast<const KV*>(vc + off));
-                    }
-                }
-            }
-        };
-        KV ka[kRounds], va[kRounds], kb[kRounds], vb[kRounds];
-        load_kv(t0, ka, va);
-
-        float acc[kMaxG][VEC];
-#pragma unroll
-        for (int h = 0; h < kMaxG; ++h)
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) acc[h][e] = 0.0f;
-        {
-            const float* qg = a.q + (size_t)m * nq * hd + (size_t)g * G * hd;
-            for (int i = tid; i < G * hd; i += kThreads) q_s[i] = load_sc1(qg + i);
-        }
-        if (tid < 16) { m_s[tid] = -INFINITY; l_s[tid] = 0.0f; }
-        __syncthreads();
-        if (u == (int)blockIdx.x) mark(a, bar, 0);
-
-        auto pass = [&](int c0, const KV (&kk)[kRounds], const KV (&vv)[kRounds]) {
-            const int n = min(P, t1 - c0);
-            // scores
-#pragma unroll
-            for (int rr = 0; rr < kRounds; ++rr) {
-                {
-                    const int j = rr * R + wave * TPW + tl;
-                    uint32_t kw[VEC / 2];
-                    __builtin_memcpy(kw, &kk[rr], sizeof kw);
-#pragma unroll
-                    for (int h = 0; h < kMaxG; ++h) {
-                        if (h < G) {
-                            const float* qh = q_s + h * hd + dl * VEC;
-                            float d = 0.0f;
-#pragma unroll
-                            for (int e = 0; e < VEC / 2; ++e) {
-                                const half2_t k2 = as_half2(kw[e]);
-                                d = fmaf(qh[2 * e], (float)k2.x, d);
-                                d = fmaf(qh[2 * e + 1], (float)k2.y, d);
-                            }
-#pragma unroll
-                            for (int o = 1; o < LPT; o <<= 1) d += __shfl_xor(d, o, 64);
-                            if (dl == 0 && j < n) p_s[h * P + j] = d * scale;
-                        }
-                    }
-                }
-            }
-            __syncthreads();
-            // online softmax, one wave per head
-            for (int h = wave; h < G; h += kWaves) {
-                float mx = -INFINITY;
-                for (int j = lane; j < n; j += 64) mx = fmaxf(mx, p_s[h * P + j]);
-                mx = wave_max(mx);
-                const float mold = m_s[h];
-                const float mnew = fmaxf(mold, mx);
-                float sum = 0.0f;
-                for (int j = lane; j < n; j += 64) {
-                    const float e = expf(p_s[h * P + j] - mnew);
-                    p_s[h * P + j] = e;
-                    sum += e;
-                }
-                sum = wave_sum(sum);
-                if (lane == 0) {
-                    const float alpha = expf(mold - mnew);  // 0 on the first pass
-                    a_s[h] = alpha;
-                    l_s[h] = l_s[h] * alpha + sum;
-                    m_s[h] = mnew;
-                }
-            }
-            __syncthreads();
-            // acc = alpha * acc + sum_j p[j] v[j] over this lane's tokens
-#pragma unroll
-            for (int h = 0; h < kMaxG; ++h)
-                if (h < G) {
-                    const float al = a_s[h];
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e) acc[h][e] *= al;
-                }
-#pragma unroll
-            for (int rr = 0; rr < kRounds; ++rr) {
-                {
-                    const int j = rr * R + wave * TPW + tl;
-                    if (j < n) {
-                        uint32_t vw[VEC / 2];
-                        __builtin_memcpy(vw, &vv[rr], sizeof vw);
-#pragma unroll
-                        for (int h = 0; h < kMaxG; ++h) {
-                            if (h < G) {
-                                const float pj = p_s[h * P + j];
-#pragma unroll
-                                for (int e = 0; e < VEC / 2; ++e) {
-                                    const half2_t v2 = as_half2(vw[e]);
-                                    acc[h][2 * e] = fmaf(pj, (float)v2.x, acc[h][2 * e]);
-                                    acc[h][2 * e + 1] = fmaf(pj, (float)v2.y, acc[h][2 * e + 1]);
-                                }
-                            }
-                        }
-                    }
-                }
-            }
-            __syncthreads();  // p_s is rewritten by the next pass
-        };
-        for (int c0 = t0; c0 < t1; c0 += 2 * P) {
-            if (c0 + P < t1) load_kv(c0 + P, kb, vb);
-            pass(c0, ka, va);
-            if (c0 + P >= t1) break;
-            if (c0 + 2 * P < t1) load_kv(c0 + 2 * P, ka, va);
-            pass(c0 + P, kb, vb);
-        }
-        if (u == (int)blockIdx.x) mark(a, bar, 1);
-        // reduce over the tokens of a wave, then over waves (in wave order)
-#pragma unroll
-        for (int h = 0; h < kMaxG; ++h)
-            if (h < G)
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    float x = acc[h][e];
-#pragma unroll
-                    for (int o = LPT; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
-                    acc[h][e] = x;
-                }
-        if (tl == 0)
-#pragma unroll
-            for (int h = 0; h < kMaxG; ++h)
-                if (h < G)
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e) o_s[(size_t)wave * G * hd + h * hd + dl * VEC + e] = acc[h][e];
-        __syncthreads();
-        const size_t grp = (size_t)m * nkv + g;
-        float* ml = a.attn_ml + (grp * MS + s) * G * 2;
-        float* pa = a.attn_acc + (grp * MS + s) * (size_t)G * hd;
-        if (tid < G) { store_sc1(&ml[2 * tid], m_s[tid]); store_sc1(&ml[2 * tid + 1], l_s[tid]); }
-        for (int idx = tid; idx < G * hd; idx += kThreads) {
-            float o = 0.0f;
-            for (int w = 0; w < kWaves; ++w) o += o_s[(size_t)w * G * hd + idx];
-            store_sc1(&pa[idx], o);
-        }
-        __syncthreads();  // o_s / q_s are rewritten by the next unit
-    }
-    return true;
+// Context split of a row: splits of at least split_tokens tokens (a
+// multiple of the pass size), at most kAttnMaxSplits of them; a row's
+// arithmetic depends only on its own context length.
+__device__ __forceinline__ int split_size(int ctx, int split_tokens, int pass) {
+    int t = (ctx + kAttnMaxSplits - 1) / kAttnMaxSplits;
+    t = (t + pass - 1) / pass * pass;
+    return t > split_tokens ? t : split_tokens;
 }
-
-// ------------------------------------------------------------ epilogues
 
 // CPU's rotation with separately rounded products (no FMA).
 __device__ __forceinline__ float rot_lo(float a, float b, float c, float s) {
@@ -931,13 +804,357 @@ __device__ __forceinline__ float rot_hi(float a, float b, float c, float s) {
     return b * c + a * s;
 }
 
-struct Best {
-    float v;
-    int i;
-};
-__device__ __forceinline__ Best better(Best x, Best y) {
-    if (y.v > x.v || (y.v == x.v && y.i < x.i)) return y;
-    return x;
+// One attention unit per (row, kv head, context split); the G query heads of
+// the group share every K/V element it loads. A unit requests its first K/V
+// tile, then polls the raw q (and, for the unit that holds the current
+// position, k and v) sums of the QKV phase, adds the bias and applies RoPE
+// (the last unit also appends the row to the paged cache). Tokens go in
+// passes of kPass: the pass's K and V rows are staged in LDS (16-byte loads,
+// the next pass's requested before the current one is computed); scores run
+// one lane per token (wave h = head h), the online softmax per head in that
+// wave, and P.V one thread per (head, dim pair) output, so no cross-lane
+// reductions are needed. The last split of a row's kv head merges the
+// others' tagged partials, in split order, into the output.
+template <int M, int HD>
+__device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const lyk_step_layer& Lw, uint32_t tag) {
+    const int tid = phase_tid();
+    constexpr int P = kPass;
+    constexpr int KS = HD + 2;                     // padded LDS row of K (halves): no bank conflicts
+    constexpr int CPR = HD / 8 > 0 ? HD / 8 : 1;   // 16-byte pieces per K/V row
+    constexpr int VB = HD % 8 == 0 ? 16 : HD * 2;  // bytes per piece
+    constexpr int kLoads = (P * CPR + kThreads - 1) / kThreads;
+    constexpr int kPairs = (16 * HD / 2 + kThreads - 1) / kThreads;  // (head, dim pair) per thread, G <= 16
+    constexpr int half = HD / 2;
+    using Piece = typename std::conditional<(VB == 16), u32x4,
+                                            typename std::conditional<(VB == 8), u64, uint32_t>::type>::type;
+    static_assert(HD % 8 == 0 || HD * 2 <= 16, "head dim");
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float m_s[16], l_s[16], a_s[16];
+    __shared__ float ml_all[kAttnMaxSplits][16][2];
+    mark(a, ph, 0);
+    const int nq = a.md.num_heads, nkv = a.md.num_kv_heads;
+    const int G = nq / nkv, bt = a.md.block_tokens;
+    const int lane = tid & 63, wave = tid >> 6;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int GH = G * HD;
+    float* q_s = reinterpret_cast<float*>(smem);                  // [G][HD] rotated queries
+    float* p_s = q_s + GH;                                         // [G][P] softmax weights
+    float* k_f = p_s + G * P;                                      // [HD] current key, fp32
+    uint16_t* ks = reinterpret_cast<uint16_t*>(k_f + HD);          // [P][KS] K tile
+    uint16_t* vs = ks + P * KS;                                    // [P][HD] V tile
+    uint16_t* kcur = vs + P * HD;                                  // [HD] current key, fp16
+    uint16_t* vcur = kcur + HD;                                    // [HD] current value, fp16
+    float* part = reinterpret_cast<float*>(smem);                  // [kAttnMaxSplits][GH] merge
+    const int kq = nq * HD, rows = (nq + 2 * nkv) * HD;
+
+    int S[M], T[M], ctxs[M], units = 0;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        ctxs[m] = ld(a.io.positions + m) + 1;
+        T[m] = split_size(ctxs[m], a.attn_split_tokens, P);
+        S[m] = (ctxs[m] + T[m] - 1) / T[m];
+        units += nkv * S[m];
+    }
+    bool ok = true;
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        int m = 0, r = u, Sm = S[0], Tm = T[0], ctx = ctxs[0];
+#pragma unroll
+        for (int mm = 1; mm < M; ++mm)
+            if (m == mm - 1 && r >= nkv * Sm) {
+                r -= nkv * Sm;
+                m = mm;
+                Sm = S[mm];
+                Tm = T[mm];
+                ctx = ctxs[mm];
+            }
+        const int g = r / Sm, s = r % Sm;
+        const int pos = ctx - 1;
+        const int t0 = s * Tm, t1 = min(ctx, t0 + Tm);
+        const bool last = s == Sm - 1;   // holds the current position
+        const int* tab = a.io.block_tables + (size_t)m * a.io.table_stride;
+        const size_t head_stride = (size_t)bt * HD;   // one kv head of a block
+        const size_t blk_stride = (size_t)nkv * head_stride;
+        const uint16_t* kc = Lw.k_cache + (size_t)g * head_stride;
+        const uint16_t* vc = Lw.v_cache + (size_t)g * head_stride;
+
+        // this thread's pieces of the K/V rows of the pass at c0 (the
+        // current position's row comes from LDS when staged)
+        auto load_kv = [&](int c0, Piece (&kk)[kLoads], Piece (&vv)[kLoads]) {
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) {
+                const int e = tid + i * kThreads, j = e / CPR, c = e % CPR;
+                const int t = c0 + j;
+                if (j < P && t < t1 && t != pos) {
+                    const size_t off = (size_t)ld(tab + t / bt) * blk_stride + (size_t)(t % bt) * HD + c * (VB / 2);
+                    kk[i] = ld(reinterpret_cast<const Piece*>(kc + off));
+                    vv[i] = ld(reinterpret_cast<const Piece*>(vc + off));
+                }
+            }
+        };
+        auto stage = [&](int c0, const Piece (&kk)[kLoads], const Piece (&vv)[kLoads]) {
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) {
+                const int e = tid + i * kThreads, j = e / CPR, c = e % CPR;
+                const int t = c0 + j;
+                if (j < P && t < t1) {
+                    Piece kp = kk[i], vp = vv[i];
+                    if (t == pos) {
+                        __builtin_memcpy(&kp, kcur + c * (VB / 2), VB);
+                        __builtin_memcpy(&vp, vcur + c * (VB / 2), VB);
+                    }
+                    uint32_t kw[VB / 4], vw[VB / 4];
+                    __builtin_memcpy(kw, &kp, VB);
+                    __builtin_memcpy(vw, &vp, VB);
+                    uint32_t* kd = reinterpret_cast<uint32_t*>(ks + j * KS + c * (VB / 2));
+                    uint32_t* vd = reinterpret_cast<uint32_t*>(vs + j * HD + c * (VB / 2));
+#pragma unroll
+                    for (int w = 0; w < VB / 4; ++w) {
+                        kd[w] = kw[w];
+                        vd[w] = vw[w];
+                    }
+                }
+            }
+        };
+        Piece ka[kLoads], va[kLoads];
+        load_kv(t0, ka, va);
+
+        // raw q (and current k, v) sums + bias, polled
+        const u64* src = a.qkv + (size_t)m * rows;
+        {
+            const int nw = GH + (last ? 2 * HD : 0);
+            for (int e0 = tid; e0 < nw; e0 += kThreads * 4) {
+                uint32_t v[4];
+                uint32_t have = 0;
+                int idx[4];
+#pragma unroll
+                for (int u2 = 0; u2 < 4; ++u2) {
+                    const int e = e0 + u2 * kThreads;
+                    idx[u2] = e < GH ? g * GH + e : (e < GH + HD ? kq + g * HD + (e - GH) : kq + nkv * HD + g * HD + (e - GH - HD));
+                }
+                auto pending = [&]() {
+                    int missing = 0;
+#pragma unroll
+                    for (int u2 = 0; u2 < 4; ++u2) {
+                        const int e = e0 + u2 * kThreads;
+                        if (e >= nw || (have >> u2 & 1)) continue;
+                        if (take(src + idx[u2], tag, v[u2])) have |= 1u << u2;
+                        else ++missing;
+                    }
+                    return missing;
+                };
+                ok = spin(a, pending) && ok;
+#pragma unroll
+                for (int u2 = 0; u2 < 4; ++u2) {
+                    const int e = e0 + u2 * kThreads;
+                    if (e >= nw) continue;
+                    const float x = bitsf(v[u2]) + ld(Lw.qkv_bias + idx[u2]);
+                    if (e < GH) q_s[e] = x;
+                    else if (e < GH + HD) k_f[e - GH] = x;
+                    else vcur[e - GH - HD] = f2h(x);
+                }
+            }
+        }
+        if (__syncthreads_or(!ok)) return false;
+        // RoPE on q (every head) and on the current key, from the host-built
+        // cos/sin tables; the current row goes to the paged cache
+        {
+            const float* cs = a.md.rope_cos + (size_t)pos * half;
+            const float* sn = a.md.rope_sin + (size_t)pos * half;
+            for (int e = tid; e < (G + (last ? 1 : 0)) * half; e += kThreads) {
+                const int h = e / half, i = e % half;
+                const float c = ld(cs + i), sv = ld(sn + i);
+                float* base = h < G ? q_s + h * HD : k_f;
+                const float lo = base[i], hi = base[i + half];
+                const float rl = rot_lo(lo, hi, c, sv), rh = rot_hi(lo, hi, c, sv);
+                if (h < G) {
+                    base[i] = rl;
+                    base[i + half] = rh;
+                } else {
+                    kcur[i] = f2h(rl);
+                    kcur[i + half] = f2h(rh);
+                }
+            }
+        }
+        if (tid < 16) { m_s[tid] = -INFINITY; l_s[tid] = 0.0f; }
+        __syncthreads();
+        if (last) {
+            const int blk = ld(tab + pos / bt);
+            const size_t off = (size_t)blk * blk_stride + (size_t)g * head_stride + (size_t)(pos % bt) * HD;
+            for (int i = tid; i < HD; i += kThreads) {
+                store_sc1_u16(Lw.k_cache + off + i, kcur[i]);
+                store_sc1_u16(Lw.v_cache + off + i, vcur[i]);
+            }
+        }
+        if (u == (int)blockIdx.x) mark(a, ph, 1);
+
+        float acc[kPairs][2];
+#pragma unroll
+        for (int i = 0; i < kPairs; ++i) acc[i][0] = acc[i][1] = 0.0f;
+        for (int c0 = t0; c0 < t1; c0 += P) {
+            const int n = min(P, t1 - c0);
+            stage(c0, ka, va);
+            __syncthreads();
+            if (c0 + P < t1) load_kv(c0 + P, ka, va);   // next pass, in flight meanwhile
+            // scores, one lane per token; then the online softmax of head h
+            for (int h = wave; h < G; h += kWaves) {
+                float sc = -INFINITY;
+                if (lane < n) {
+                    const float* qh = q_s + h * HD;
+                    const uint16_t* kr = ks + lane * KS;
+                    float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+                    for (int d = 0; d < HD; d += 2) {
+                        const half2_t k2 = as_half2(*reinterpret_cast<const uint32_t*>(kr + d));
+                        d0 = fmaf(qh[d], (float)k2.x, d0);
+                        d1 = fmaf(qh[d + 1], (float)k2.y, d1);
+                    }
+                    sc = (d0 + d1) * scale;
+                }
+                const float mx = wave_max(sc);
+                const float mold = m_s[h];
+                const float mnew = fmaxf(mold, mx);
+                const float pv = lane < n ? expf(sc - mnew) : 0.0f;
+                const float sum = wave_sum(pv);
+                p_s[h * P + lane] = pv;
+                if (lane == 0) {
+                    const float alpha = expf(mold - mnew);  // 0 on the first pass
+                    a_s[h] = alpha;
+                    l_s[h] = l_s[h] * alpha + sum;
+                    m_s[h] = mnew;
+                }
+            }
+            __syncthreads();
+            // acc = alpha * acc + sum_t p[h][t] V[t][d pair]
+#pragma unroll
+            for (int i = 0; i < kPairs; ++i) {
+                const int e = tid + i * kThreads;     // (head, dim pair)
+                if (e < GH / 2) {
+                    const int h = e / half, dp = e % half;
+                    const float al = a_s[h];
+                    float x0 = acc[i][0] * al, x1 = acc[i][1] * al;
+                    const float* ph_ = p_s + h * P;
+                    const uint16_t* vcol = vs + dp * 2;
+                    for (int t = 0; t < n; ++t) {
+                        const half2_t v2 = as_half2(*reinterpret_cast<const uint32_t*>(vcol + t * HD));
+                        x0 = fmaf(ph_[t], (float)v2.x, x0);
+                        x1 = fmaf(ph_[t], (float)v2.y, x1);
+                    }
+                    acc[i][0] = x0;
+                    acc[i][1] = x1;
+                }
+            }
+            __syncthreads();  // the tiles and p_s are rewritten by the next pass
+        }
+        if (u == (int)blockIdx.x) mark(a, ph, 2);
+        const size_t grp = (size_t)m * nkv + g;
+        u64* out = a.attn_out + (size_t)m * kq + (size_t)g * GH;
+        if (!last) {
+            // a partial for the row's last split to merge
+            u64* ml = a.attn_ml + (grp * kAttnMaxSplits + s) * G * 2;
+            u64* pa = a.attn_acc + (grp * kAttnMaxSplits + s) * (size_t)GH;
+            if (tid < G) {
+                put(&ml[2 * tid], fbits(m_s[tid]), tag);
+                put(&ml[2 * tid + 1], fbits(l_s[tid]), tag);
+            }
+#pragma unroll
+            for (int i = 0; i < kPairs; ++i) {
+                const int e = tid + i * kThreads;
+                if (e < GH / 2) {
+                    put(&pa[2 * e], fbits(acc[i][0]), tag);
+                    put(&pa[2 * e + 1], fbits(acc[i][1]), tag);
+                }
+            }
+        } else if (Sm == 1) {
+#pragma unroll
+            for (int i = 0; i < kPairs; ++i) {
+                const int e = tid + i * kThreads;
+                if (e < GH / 2) {
+                    const float l = l_s[e / half];
+                    put(&out[2 * e], fbits(acc[i][0] / l), tag);
+                    put(&out[2 * e + 1], fbits(acc[i][1] / l), tag);
+                }
+            }
+        } else {
+            // merge splits 0..S-1 in order: out = sum e_s acc_s / sum e_s l_s
+            if (tid < G) {
+                ml_all[Sm - 1][tid][0] = m_s[tid];
+                ml_all[Sm - 1][tid][1] = l_s[tid];
+            }
+            for (int e0 = tid; e0 < (Sm - 1) * (GH + 2 * G); e0 += kThreads * 4) {
+                uint32_t v[4];
+                uint32_t have = 0;
+                auto where = [&](int e, const u64*& w, float*& dst) {
+                    const int sp = e / (GH + 2 * G), rr = e % (GH + 2 * G);
+                    if (rr < GH) {
+                        w = a.attn_acc + (grp * kAttnMaxSplits + sp) * (size_t)GH + rr;
+                        dst = part + (size_t)sp * GH + rr;
+                    } else {
+                        const int k2 = rr - GH;
+                        w = a.attn_ml + (grp * kAttnMaxSplits + sp) * G * 2 + k2;
+                        dst = &ml_all[sp][k2 / 2][k2 % 2];
+                    }
+                };
+                auto pending = [&]() {
+                    int missing = 0;
+#pragma unroll
+                    for (int u2 = 0; u2 < 4; ++u2) {
+                        const int e = e0 + u2 * kThreads;
+                        if (e >= (Sm - 1) * (GH + 2 * G) || (have >> u2 & 1)) continue;
+                        const u64* w;
+                        float* dst;
+                        where(e, w, dst);
+                        if (take(w, tag, v[u2])) have |= 1u << u2;
+                        else ++missing;
+                    }
+                    return missing;
+                };
+                ok = spin(a, pending) && ok;
+#pragma unroll
+                for (int u2 = 0; u2 < 4; ++u2) {
+                    const int e = e0 + u2 * kThreads;
+                    if (e >= (Sm - 1) * (GH + 2 * G)) continue;
+                    const u64* w;
+                    float* dst;
+                    where(e, w, dst);
+                    *dst = bitsf(v[u2]);
+                }
+            }
+            if (__syncthreads_or(!ok)) return false;
+            if (tid < G) {
+                float mx = -INFINITY;
+                for (int sp = 0; sp < Sm; ++sp) mx = fmaxf(mx, ml_all[sp][tid][0]);
+                float L = 0.0f;
+                for (int sp = 0; sp < Sm; ++sp) {
+                    const float es = expf(ml_all[sp][tid][0] - mx);
+                    ml_all[sp][tid][0] = es;
+                    L += ml_all[sp][tid][1] * es;
+                }
+                l_s[tid] = L;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < kPairs; ++i) {
+                const int e = tid + i * kThreads;
+                if (e < GH / 2) {
+                    const int h = e / half;
+                    float o0 = 0.0f, o1 = 0.0f;
+                    for (int sp = 0; sp < Sm - 1; ++sp) {
+                        const float w = ml_all[sp][h][0];
+                        o0 += part[(size_t)sp * GH + 2 * e] * w;
+                        o1 += part[(size_t)sp * GH + 2 * e + 1] * w;
+                    }
+                    const float w = ml_all[Sm - 1][h][0];
+                    o0 += acc[i][0] * w;
+                    o1 += acc[i][1] * w;
+                    put(&out[2 * e], fbits(o0 / l_s[h]), tag);
+                    put(&out[2 * e + 1], fbits(o1 / l_s[h]), tag);
+                }
+            }
+        }
+        __syncthreads();   // LDS is rewritten by the next unit
+    }
+    mark(a, ph, 3);
+    return true;
 }
 
 // ------------------------------------------------------------ the kernel
@@ -946,207 +1163,104 @@ template <int M, bool Q8, int HD>
 __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* __restrict__ args) {
     const StepArgs& a = *args;
     if (aborted(a)) return;
-    // Every workgroup reads the barrier epoch before its first arrival;
-    // workgroup 0 advances it once the first barrier shows all have read it.
-    const uint32_t epoch = load_sc1(a.epoch);
-    if (a.io.trace && blockIdx.x == 0 && threadIdx.x == 0) st(a.io.trace, (uint64_t)__builtin_amdgcn_s_memrealtime());
     const int b = blockIdx.x;
-    const int H = a.md.hidden_size, nq = a.md.num_heads, nkv = a.md.num_kv_heads, hd = a.md.head_dim;
-    const int In = a.md.intermediate_size;
-    int bar = 0;
-    const int L = a.md.num_layers;
+    // tags of this launch: (launches completed + 1) << 8 | layer; every
+    // workgroup counts its own launches, so all agree without talking
+    const uint32_t seq = load_sc1(a.seq + b);
+    const uint32_t tag0 = (seq + 1u) << 8;
+    if (a.io.trace && threadIdx.x == 0)
+        st(a.io.trace + (size_t)b * (2 + 4 * a.phases), (uint64_t)__builtin_amdgcn_s_memrealtime());
+    const int H = a.md.hidden_size, L = a.md.num_layers;
 
-    for (int l = 0; l < L; ++l) {
-        const lyk_step_layer Lw = load_layer(a.md.layers + l);
-        float* base = a.h + (size_t)(l & 1) * kMaxRows * H;            // residual entering layer l
-        const float* prev = a.h + (size_t)((l + 1) & 1) * kMaxRows * H;  // base of layer l - 1
-        // ---- RMSNorm + fused QKV GEMV + bias + RoPE + KV append
-        {
-            const Mat A = make_mat<Q8>(Lw.qkv_w, Lw.qkv_s, (nq + 2 * nkv) * hd, H, false);
-            const int half = hd / 2, xr = half < 32 ? half : 32;
-            const int qrows = nq * hd, krows = nkv * hd;
-            const ResidualSrc rs = l == 0 ? ResidualSrc{nullptr, nullptr, nullptr, base, true}
-                                          : ResidualSrc{prev, a.d_attn, a.d_mlp, base, false};
-            const bool ok = gemv_phase<M, Q8>(
-                a, epoch, l == 0 ? -1 : bar++, A,
-                [&](const Mat& AA, const Part& pp, uint16_t* xs, int ftid) {
-                    fill_norm<M, Q8>(a, Lw.input_norm, rs, AA, pp, xs, ftid);
-                },
-                [&](int t, float (&v)[M], int lane) {
-                    const int pr = t * 64 + lane;
-                    const bool valid = pr < A.n;
-                    // packed row -> (head, natural dim): heads of hd > 64 are
-                    // stored in blocks of 64 rows holding 32 rotation pairs
-                    // (lanes j, j+32); smaller heads keep the natural order.
-                    const int head = pr / hd, e = pr % hd;
-                    int dim = e;
-                    if (hd > 64) {
-                        const int blk = e / 64, Lr = e % 64;
-                        dim = Lr < 32 ? blk * 32 + Lr : half + blk * 32 + (Lr - 32);
-                    }
-                    const float bias = valid ? ld(Lw.qkv_bias + pr) : 0.0f;
-                    const int sec = pr < qrows ? 0 : (pr < qrows + krows ? 1 : 2);
-                    const int i = dim % half;
-                    const bool lo = dim < half;
+    // the residual stream of every row, whole, in registers
+    float h[M][kNormPer];
+    {
+        const int tid = threadIdx.x;
 #pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const float val = v[m] + bias;
-                        const float other = __shfl_xor(val, xr, 64);
-                        const int pos = load_sc1(a.io.positions + m);
-                        const float c = ld(a.md.rope_cos + (size_t)pos * half + i);
-                        const float s = ld(a.md.rope_sin + (size_t)pos * half + i);
-                        const float rot = lo ? rot_lo(val, other, c, s) : rot_hi(other, val, c, s);
-                        if (!valid) continue;
-                        if (sec == 0) {
-                            store_sc1(&a.q[(size_t)m * qrows + (size_t)head * hd + dim], rot);
-                        } else {
-                            const int kvh = sec == 1 ? head - nq : head - nq - nkv;
-                            const int blk = ld(a.io.block_tables + (size_t)m * a.io.table_stride +
-                                               pos / a.md.block_tokens);
-                            const size_t off = (((size_t)blk * nkv + kvh) * a.md.block_tokens +
-                                                pos % a.md.block_tokens) * hd + dim;
-                            if (sec == 1) store_sc1_u16(Lw.k_cache + off, f2h(rot));
-                            else store_sc1_u16(Lw.v_cache + off, f2h(val));
-                        }
-                    }
-                });
-            if (!ok) return;
-        }
-        // ---- attention
-        if (!attention_phase<M, HD>(a, epoch, bar++, Lw)) return;
-        if (l == 0 && b == 0 && threadIdx.x == 0) store_sc1(a.epoch, epoch + a.barriers);
-        // ---- O GEMV (input: merged attention splits) -> attention delta
-        {
-            const Mat A = make_mat<Q8>(Lw.o_w, Lw.o_s, H, nq * hd, false);
-            const bool ok = gemv_phase<M, Q8>(
-                a, epoch, bar++, A,
-                [&](const Mat& AA, const Part& pp, uint16_t* xs, int ftid) { fill_attn<M, Q8>(a, AA, pp, xs, ftid); },
-                [&](int t, float (&v)[M], int lane) {
-                    const int r = t * 64 + lane;
-                    if (r >= H) return;
+        for (int m = 0; m < M; ++m) {
+            const float* e = a.md.embed + (size_t)load_sc1(a.io.tokens + m) * H;
 #pragma unroll
-                    for (int m = 0; m < M; ++m) store_sc1(&a.d_attn[(size_t)m * H + r], v[m]);
-                });
-            if (!ok) return;
-        }
-        // ---- RMSNorm + gate/up GEMV + SiLU
-        {
-            const Mat A = make_mat<Q8>(Lw.gateup_w, Lw.gateup_s, In, H, true);
-            const ResidualSrc rs{base, a.d_attn, nullptr, nullptr, false};
-            const bool ok = gemv_phase<M, Q8>(
-                a, epoch, bar++, A,
-                [&](const Mat& AA, const Part& pp, uint16_t* xs, int ftid) {
-                    fill_norm<M, Q8>(a, Lw.post_norm, rs, AA, pp, xs, ftid);
-                },
-                [&](int t, float (&v)[M], int lane) {
-                    const int j = t * 32 + lane;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const float u = __shfl_down(v[m], 32, 64);
-                        if (lane < 32 && j < In) {
-                            const float g = v[m];
-                            store_sc1_u16(&a.act[(size_t)m * a.ld_act + j], f2h(g / (1.0f + expf(-g)) * u));
-                        }
-                    }
-                });
-            if (!ok) return;
-        }
-        // ---- down GEMV -> MLP delta
-        {
-            const Mat A = make_mat<Q8>(Lw.down_w, Lw.down_s, H, In, false);
-            const bool ok = gemv_phase<M, Q8>(
-                a, epoch, bar++, A,
-                [&](const Mat& AA, const Part& pp, uint16_t* xs, int ftid) { fill_copy<M, Q8>(a.act, a.ld_act, AA, pp, xs, ftid); },
-                [&](int t, float (&v)[M], int lane) {
-                    const int r = t * 64 + lane;
-                    if (r >= H) return;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) store_sc1(&a.d_mlp[(size_t)m * H + r], v[m]);
-                });
-            if (!ok) return;
-        }
-    }
-    if (a.io.mode == LYK_STEP_HIDDEN) {
-        if (a.io.trace && b == 0 && threadIdx.x == 0) st(a.io.trace + bar + 1, (uint64_t)__builtin_amdgcn_s_memrealtime());
-        return;
-    }
-
-    // ---- final norm + LM head (+ per-tile greedy candidates)
-    const int V = a.md.vocab_size;
-    const bool greedy = a.io.mode == LYK_STEP_GREEDY;
-    const Mat A = make_mat<Q8>(a.md.lm_head_w, a.md.lm_head_s, V, H, false);
-    const ResidualSrc rs{a.h + (size_t)((L - 1) & 1) * kMaxRows * H, a.d_attn, a.d_mlp, nullptr, false};
-    const bool ok = gemv_phase<M, Q8>(
-        a, epoch, bar++, A,
-        [&](const Mat& AA, const Part& pp, uint16_t* xs, int ftid) {
-            fill_norm<M, Q8>(a, a.md.final_norm, rs, AA, pp, xs, ftid);
-        },
-        [&](int t, float (&v)[M], int lane) {
-            const int r = t * 64 + lane;
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                if (r < V) st(a.io.logits + (size_t)m * a.io.ld_logits + r, v[m]);
-                if (!greedy) continue;
-                float x = v[m];
-                int bad = 0;
-                if (r < V && !isfinite(x)) {
-                    bad = 1;
-                    if (isnan(x)) x = -INFINITY;
-                }
-                Best bst = r < V ? Best{x, r} : Best{-INFINITY, 0x7fffffff};
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) bst = better(bst, Best{__shfl_xor(bst.v, o, 64), __shfl_xor(bst.i, o, 64)});
-                bad = (int)wave_sum((float)bad);
-                if (lane == 0) {
-                    const size_t sl = (size_t)m * A.tiles + t;
-                    store_sc1(&a.best_v[sl], bst.v);
-                    store_sc1(&a.best_i[sl], bst.i);
-                    store_sc1(&a.best_bad[sl], bad);
-                }
+            for (int j = 0; j < kNormPer; ++j) {
+                const int i = tid + j * kThreads;
+                h[m][j] = i < H ? ld(e + i) : 0.0f;
             }
-        });
-    if (!ok) return;
-    if (!greedy) {
-        if (a.io.trace && b == 0 && threadIdx.x == 0) st(a.io.trace + bar + 1, (uint64_t)__builtin_amdgcn_s_memrealtime());
-        return;
-    }
-    if (!grid_sync(a, epoch, (uint32_t)bar++)) return;
-    if (b != 0) return;
-    // ---- greedy token of row 0 (M == 1): first index of the maximum
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ float bv[kWaves];
-    __shared__ int bi[kWaves], bb[kWaves];
-    Best bst{-INFINITY, 0x7fffffff};
-    int bad = 0;
-    for (int t = tid; t < A.tiles; t += kThreads) {
-        bst = better(bst, Best{load_sc1(&a.best_v[t]), load_sc1_i32(&a.best_i[t])});
-        bad += load_sc1_i32(&a.best_bad[t]);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) bst = better(bst, Best{__shfl_xor(bst.v, o, 64), __shfl_xor(bst.i, o, 64)});
-    bad = (int)wave_sum((float)bad);
-    if (lane == 0) { bv[wave] = bst.v; bi[wave] = bst.i; bb[wave] = bad; }
-    __syncthreads();
-    if (tid == 0) {
-        Best r{bv[0], bi[0]};
-        int nb = bb[0];
-        for (int w = 1; w < kWaves; ++w) { r = better(r, Best{bv[w], bi[w]}); nb += bb[w]; }
-        const int token = r.i < V ? r.i : 0;
-        // device-scope stores: the next step may run on other XCDs
-        store_sc1(a.io.tokens, token);
-        store_sc1(a.io.positions, load_sc1(a.io.positions) + 1);
-        if (a.io.nonfinite) st(a.io.nonfinite, ld(a.io.nonfinite) + nb);
-        if (a.io.history && a.io.step) {
-            const int s = ld(a.io.step);
-            st(a.io.history + s, token);
-            st(a.io.step, s + 1);
         }
-        if (a.io.trace) st(a.io.trace + bar + 1, (uint64_t)__builtin_amdgcn_s_memrealtime());
     }
+
+    // per layer: QKV, attention, O, gate/up, down; then the LM head
+    const int nph = 5 * L + (a.io.mode == LYK_STEP_HIDDEN ? 0 : 1);
+    lyk_step_layer Lw = load_layer(a.md.layers);
+#pragma nounroll
+    for (int ph = 0; ph < nph; ++ph) {
+        const int l = ph / 5, kind = ph < 5 * L ? ph % 5 : (int)kHead;
+        if (kind == kQkv && l > 0) Lw = load_layer(a.md.layers + l);
+        const bool ok = kind == kAttn ? attention_phase<M, HD>(a, ph, Lw, tag0 | (uint32_t)l)
+                                      : gemv_step<M, Q8>(a, ph, kind, l, Lw, h, tag0);
+        if (!ok) return;
+    }
+
+    if (a.io.mode == LYK_STEP_GREEDY && b == 0) {
+        // ---- greedy token of row 0 (M == 1): first index of the maximum
+        const int V = a.md.vocab_size, tiles = (V + 63) / 64;
+        const uint32_t htag = tag0 | (uint32_t)L;
+        mark(a, nph, 0);
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        __shared__ float bv[kWaves];
+        __shared__ int bi[kWaves], bb[kWaves];
+        Best bst{-INFINITY, 0x7fffffff};
+        int bad = 0;
+        bool good = true;
+        for (int t = tid; t < tiles; t += kThreads) {
+            uint32_t w[3];
+            uint32_t have = 0;
+            auto pending = [&]() {
+                int missing = 0;
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    if (have >> k & 1) continue;
+                    if (take(a.best + (size_t)t * 3 + k, htag, w[k])) have |= 1u << k;
+                    else ++missing;
+                }
+                return missing;
+            };
+            good = spin(a, pending) && good;
+            bst = better(bst, Best{bitsf(w[0]), (int)w[1]});
+            bad += (int)w[2];
+        }
+        // The token and position change only after every other workgroup
+        // has finished this launch (and so read them).
+        for (int w = tid + 1; w < (int)gridDim.x; w += kThreads) {
+            auto pending = [&]() { return load_sc1(a.seq + w) == seq + 1u ? 0 : 1; };
+            good = spin(a, pending) && good;
+        }
+        if (__syncthreads_or(!good)) return;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) bst = better(bst, Best{__shfl_xor(bst.v, o, 64), __shfl_xor(bst.i, o, 64)});
+        bad = (int)wave_sum((float)bad);
+        if (lane == 0) { bv[wave] = bst.v; bi[wave] = bst.i; bb[wave] = bad; }
+        __syncthreads();
+        if (tid == 0) {
+            Best r{bv[0], bi[0]};
+            int nb = bb[0];
+            for (int w = 1; w < kWaves; ++w) { r = better(r, Best{bv[w], bi[w]}); nb += bb[w]; }
+            const int token = r.i < V ? r.i : 0;
+            store_sc1(a.io.tokens, token);
+            store_sc1(a.io.positions, ld(a.io.positions) + 1);
+            if (a.io.nonfinite) st(a.io.nonfinite, ld(a.io.nonfinite) + nb);
+            if (a.io.history && a.io.step) {
+                const int s = ld(a.io.step);
+                st(a.io.history + s, token);
+                st(a.io.step, s + 1);
+            }
+        }
+        mark(a, nph, 3);
+    }
+    if (threadIdx.x == 0) store_sc1(a.seq + b, seq + 1u);
+    if (a.io.trace && threadIdx.x == 0)
+        st(a.io.trace + (size_t)b * (2 + 4 * a.phases) + 1, (uint64_t)__builtin_amdgcn_s_memrealtime());
 }
 
 // ------------------------------------------------------------ host side
-
 
 int chunks_of(int64_t k, bool q8) {
     const int unit = q8 ? 16 : 32;
@@ -1154,12 +1268,6 @@ int chunks_of(int64_t k, bool q8) {
 }
 
 int vec_of(int hd) { return hd % 8 == 0 ? 8 : 2; }
-
-// Tokens per attention pass (the kernel's P for this head dim).
-int pass_tokens(int hd) {
-    const int lpt = hd / vec_of(hd), tpw = 64 / lpt, R = kWaves * tpw;
-    return R >= 64 ? R : R * (64 / R);
-}
 
 // Head dims with a compiled attention path.
 bool head_dim_supported(int hd) { return hd == 4 || hd == 64 || hd == 128; }
@@ -1190,51 +1298,9 @@ int check_model(const lyk_step_model& md) {
     const int vec = vec_of(hd);
     if (!head_dim_supported(hd)) return LYK_ERR_SHAPE;
     if (G > (64 / vec < 16 ? 64 / vec : 16)) return LYK_ERR_SHAPE;
-    if (md.hidden_size > kNormPer * kThreads || (md.intermediate_size & 1) ||
-        ((int64_t)md.num_heads * hd) & 1)
+    if (md.hidden_size > kNormPer * kThreads || (md.intermediate_size & 1) || md.num_layers > 255)
         return LYK_ERR_SHAPE;
     return LYK_OK;
-}
-
-struct Layout {
-    uint64_t err, epoch, args, bar, tile_cnt, part, attn_ml, attn_acc, h, d_attn, d_mlp, q, act, best_v,
-        best_i, best_bad, total;
-    int ld_act, head_tiles;
-};
-
-Layout layout(const lyk_step_model& md, int rows, int grid) {
-    Layout L{};
-    const bool q8 = md.q8 != 0;
-    const int ck = q8 ? 128 : 256;
-    const int nq = md.num_heads, nkv = md.num_kv_heads, hd = md.head_dim, G = nq / nkv;
-    L.ld_act = chunks_of(md.intermediate_size, q8) * ck;
-    L.head_tiles = (md.vocab_size + 63) / 64;
-    const int tiles_max = std::max({L.head_tiles, (md.intermediate_size + 31) / 32,
-                                    (md.hidden_size + 63) / 64, ((nq + 2 * nkv) * hd + 63) / 64});
-    uint64_t at = 0;
-    auto take = [&](uint64_t bytes) {
-        const uint64_t o = at;
-        at += (bytes + 255) / 256 * 256;
-        return o;
-    };
-    L.err = take(4);
-    L.epoch = take(4);
-    L.args = take(sizeof(StepArgs));
-    L.bar = take((uint64_t)kBarLines * kLineWords * 4);
-    L.tile_cnt = take((uint64_t)tiles_max * 4);
-    L.part = take((uint64_t)grid * 2 * rows * 64 * 4);
-    L.attn_ml = take((uint64_t)rows * nkv * kAttnMaxSplits * G * 2 * 4);
-    L.attn_acc = take((uint64_t)rows * nkv * kAttnMaxSplits * G * hd * 4);
-    L.h = take((uint64_t)2 * kMaxRows * md.hidden_size * 4);
-    L.d_attn = take((uint64_t)rows * md.hidden_size * 4);
-    L.d_mlp = take((uint64_t)rows * md.hidden_size * 4);
-    L.q = take((uint64_t)rows * nq * hd * 4);
-    L.act = take((uint64_t)rows * L.ld_act * 2);
-    L.best_v = take((uint64_t)rows * L.head_tiles * 4);
-    L.best_i = take((uint64_t)rows * L.head_tiles * 4);
-    L.best_bad = take((uint64_t)rows * L.head_tiles * 4);
-    L.total = at;
-    return L;
 }
 
 // The five GEMVs of a step: {rows, k, paired}.
@@ -1252,40 +1318,82 @@ void step_mats(const lyk_step_model& md, MatShape (&out)[5]) {
     out[4] = {md.vocab_size, H, false};
 }
 
-// Largest chunk range of one workgroup in a phase (as partition() cuts it).
-int64_t max_range(const MatShape& mt, bool q8, int grid, int64_t* chunks_out) {
-    const int64_t tiles = mt.paired ? (mt.n + 31) / 32 : (mt.n + 63) / 64;
-    const int64_t chunks = chunks_of(mt.k, q8);
-    const int64_t U = tiles * chunks;
-    *chunks_out = chunks;
-    if (tile_aligned(tiles, chunks, grid)) return (tiles + grid - 1) / grid * chunks;
-    const int64_t gp = U < grid ? U : grid;
-    return (U + gp - 1) / gp;
+struct PhaseShape {
+    int64_t tiles, chunks, range, win;  // range: chunks of one workgroup, at most
+    int pieces;
+};
+PhaseShape phase_shape(const MatShape& mt, bool q8, int grid) {
+    PhaseShape ps;
+    ps.tiles = mt.paired ? (mt.n + 31) / 32 : (mt.n + 63) / 64;
+    ps.chunks = chunks_of(mt.k, q8);
+    ps.pieces = tile_pieces(ps.tiles, ps.chunks, grid);
+    if (ps.pieces == 1) {
+        const int64_t gp = ps.tiles < grid ? ps.tiles : grid;
+        ps.range = (ps.tiles + gp - 1) / gp * ps.chunks;
+        ps.win = ps.chunks;
+    } else {
+        ps.range = (ps.chunks + ps.pieces - 1) / ps.pieces;
+        ps.win = ps.range;
+    }
+    return ps;
 }
 
-// Dynamic LDS of a launch: the largest x window (plus, for the O phase, the
-// split-merge weights) or reduction buffer of any GEMV phase, or the
-// attention buffers.
+struct Layout {
+    uint64_t err, seq, args, qkv, attn_ml, attn_acc, attn_out, d_attn, d_mlp, act, dpart, best, total;
+    uint64_t dpart_stride;   // in words
+};
+
+Layout layout(const lyk_step_model& md, int rows, int grid) {
+    Layout L{};
+    const bool q8 = md.q8 != 0;
+    const int64_t nq = md.num_heads, nkv = md.num_kv_heads, hd = md.head_dim, G = nq / nkv;
+    const int64_t H = md.hidden_size;
+    MatShape mats[5];
+    step_mats(md, mats);
+    uint64_t dpart_words = 1;
+    for (const MatShape& mt : mats) {
+        const PhaseShape ps = phase_shape(mt, q8, grid);
+        if (ps.pieces > 1) dpart_words = std::max<uint64_t>(dpart_words, (uint64_t)ps.tiles * ps.pieces * rows * 64);
+    }
+    L.dpart_stride = (dpart_words * 8 + 255) / 256 * 256 / 8;
+    const int64_t head_tiles = (md.vocab_size + 63) / 64;
+    uint64_t at = 0;
+    auto take = [&](uint64_t bytes) {
+        const uint64_t o = at;
+        at += (bytes + 255) / 256 * 256;
+        return o;
+    };
+    L.err = take(4);
+    L.seq = take((uint64_t)grid * 4);
+    L.args = take(sizeof(StepArgs));
+    L.qkv = take((uint64_t)rows * (nq + 2 * nkv) * hd * 8);
+    L.attn_ml = take((uint64_t)rows * nkv * kAttnMaxSplits * G * 2 * 8);
+    L.attn_acc = take((uint64_t)rows * nkv * kAttnMaxSplits * G * hd * 8);
+    L.attn_out = take((uint64_t)rows * nq * hd * 8);
+    L.d_attn = take((uint64_t)md.num_layers * kMaxRows * H * 8);
+    L.d_mlp = take((uint64_t)md.num_layers * kMaxRows * H * 8);
+    L.act = take((uint64_t)rows * (md.intermediate_size / 2) * 8);
+    L.dpart = take((uint64_t)5 * L.dpart_stride * 8);
+    L.best = take((uint64_t)rows * head_tiles * 3 * 8);
+    L.total = at;
+    return L;
+}
+
+// Dynamic LDS of a launch: the largest x window or reduction buffer of any
+// GEMV phase, or the attention buffers.
 size_t lds_bytes(const lyk_step_model& md, int rows, int grid) {
     const bool q8 = md.q8 != 0;
     const int ck = q8 ? 128 : 256;
     MatShape mats[5];
     step_mats(md, mats);
     size_t need = (size_t)kWaves * kPieces * rows * 64 * 4;
-    for (int i = 0; i < 5; ++i) {
-        int64_t chunks = 0;
-        const int64_t per = max_range(mats[i], q8, grid, &chunks);
-        const int64_t win = per >= chunks ? chunks : per;
-        size_t bytes = (size_t)rows * win * ck * 2;
-        if (i == 1) {  // O phase: merge weights of the heads in the window
-            const int64_t nh = std::min<int64_t>(md.num_heads, (win * ck + md.head_dim - 1) / md.head_dim + 1);
-            bytes += (size_t)rows * nh * (kAttnMaxSplits + 1) * 4;
-        }
-        need = std::max(need, bytes);
+    for (const MatShape& mt : mats) {
+        const PhaseShape ps = phase_shape(mt, q8, grid);
+        need = std::max(need, (size_t)rows * ps.win * ck * 2);
     }
-    const int G = md.num_heads / md.num_kv_heads, hd = md.head_dim;
-    need = std::max(need, (size_t)G * (pass_tokens(hd) + hd) * 4);
-    need = std::max(need, (size_t)kWaves * G * hd * 4);
+    const size_t G = md.num_heads / md.num_kv_heads, hd = md.head_dim, P = kPass;
+    need = std::max(need, (G * hd + G * P + hd) * 4 + (P * (hd + 2) + P * hd + 2 * hd) * 2);
+    need = std::max(need, (size_t)kAttnMaxSplits * G * hd * 4);
     return need;
 }
 
@@ -1295,10 +1403,9 @@ bool pieces_ok(const lyk_step_model& md, int grid) {
     MatShape mats[5];
     step_mats(md, mats);
     for (const MatShape& mt : mats) {
-        int64_t chunks = 0;
-        const int64_t per = max_range(mt, q8, grid, &chunks);
-        const int64_t lw = (per + kWaves - 1) / kWaves;   // chunks per wave, at most
-        if (1 + (lw - 1 + chunks - 1) / chunks > kPieces) return false;
+        const PhaseShape ps = phase_shape(mt, q8, grid);
+        const int64_t lw = (ps.range + kWaves - 1) / kWaves;   // chunks per wave, at most
+        if (1 + (lw - 1 + ps.chunks - 1) / ps.chunks > kPieces) return false;
     }
     return true;
 }
@@ -1357,18 +1464,19 @@ extern "C" {
 uint64_t lyk_hip_step_workspace_bytes(const lyk_step_model* model, int max_rows) {
     if (!model || max_rows < 1 || max_rows > kMaxRows || check_model(*model) != LYK_OK) return 0;
     const int grid = step_grid();
-    if (grid < 1) return 0;
+    if (grid < kAttnMaxSplits || !pieces_ok(*model, grid)) return 0;
+    if (lds_bytes(*model, max_rows, grid) > kMaxDynamicLds) return 0;
     return layout(*model, max_rows, grid).total;
 }
 
-uint32_t lyk_hip_step_barriers(const lyk_step_model* model, int mode) {
+uint32_t lyk_hip_step_phases(const lyk_step_model* model, int mode) {
     if (!model) return 0;
-    // per layer: before attention, O, gate/up, down, and before the next
-    // layer's QKV; the last of these is the LM head's (LOGITS, GREEDY); the
-    // greedy argmax waits for one more
-    const uint32_t layers = (uint32_t)model->num_layers * 5u;
-    return mode == LYK_STEP_HIDDEN ? layers - 1u : (mode == LYK_STEP_GREEDY ? layers + 1u : layers);
+    // per layer QKV, attention, O, gate/up, down; the LM head; the argmax
+    return (uint32_t)model->num_layers * 5u + (mode == LYK_STEP_HIDDEN ? 0u : 1u) +
+           (mode == LYK_STEP_GREEDY ? 1u : 0u);
 }
+
+int lyk_hip_step_grid(void) { return step_grid(); }
 
 int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void* d_workspace,
                         uint64_t workspace_bytes, int max_rows, void* stream) {
@@ -1384,11 +1492,11 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     if (io->mode == LYK_STEP_GREEDY && m != 1) return LYK_ERR_INVALID_ARG;
     const int grid = step_grid();
     if (grid < 1) return LYK_ERR_HIP;
-    if (!pieces_ok(*model, grid)) return LYK_ERR_SHAPE;
+    if (grid < kAttnMaxSplits || !pieces_ok(*model, grid)) return LYK_ERR_SHAPE;
     const Layout L = layout(*model, max_rows, grid);
     if (L.total > workspace_bytes) return LYK_ERR_WORKSPACE;
     const size_t lds = lds_bytes(*model, m, grid);
-    if (lds > 48 * 1024) return LYK_ERR_SHAPE;
+    if (lds > kMaxDynamicLds) return LYK_ERR_SHAPE;
 
     char* ws = static_cast<char*>(d_workspace);
     StepArgs a;
@@ -1396,24 +1504,19 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     a.md = *model;
     a.io = *io;
     a.err = reinterpret_cast<int*>(ws + L.err);
-    a.epoch = reinterpret_cast<uint32_t*>(ws + L.epoch);
-    a.bar = reinterpret_cast<unsigned*>(ws + L.bar);
-    a.tile_cnt = reinterpret_cast<unsigned*>(ws + L.tile_cnt);
-    a.part = reinterpret_cast<float*>(ws + L.part);
-    a.attn_ml = reinterpret_cast<float*>(ws + L.attn_ml);
-    a.attn_acc = reinterpret_cast<float*>(ws + L.attn_acc);
-    a.h = reinterpret_cast<float*>(ws + L.h);
-    a.d_attn = reinterpret_cast<float*>(ws + L.d_attn);
-    a.d_mlp = reinterpret_cast<float*>(ws + L.d_mlp);
-    a.q = reinterpret_cast<float*>(ws + L.q);
-    a.act = reinterpret_cast<uint16_t*>(ws + L.act);
-    a.best_v = reinterpret_cast<float*>(ws + L.best_v);
-    a.best_i = reinterpret_cast<int*>(ws + L.best_i);
-    a.best_bad = reinterpret_cast<int*>(ws + L.best_bad);
-    a.ld_act = L.ld_act;
+    a.seq = reinterpret_cast<uint32_t*>(ws + L.seq);
+    a.qkv = reinterpret_cast<u64*>(ws + L.qkv);
+    a.attn_ml = reinterpret_cast<u64*>(ws + L.attn_ml);
+    a.attn_acc = reinterpret_cast<u64*>(ws + L.attn_acc);
+    a.attn_out = reinterpret_cast<u64*>(ws + L.attn_out);
+    a.d_attn = reinterpret_cast<u64*>(ws + L.d_attn);
+    a.d_mlp = reinterpret_cast<u64*>(ws + L.d_mlp);
+    a.act = reinterpret_cast<u64*>(ws + L.act);
+    a.dpart = reinterpret_cast<u64*>(ws + L.dpart);
+    a.dpart_stride = (size_t)L.dpart_stride;
+    a.best = reinterpret_cast<u64*>(ws + L.best);
     a.attn_split_tokens = kAttnSplitTokens;
-    a.attn_max_splits = kAttnMaxSplits;
-    a.barriers = lyk_hip_step_barriers(model, io->mode);
+    a.phases = (int)lyk_hip_step_phases(model, io->mode);
     hipStream_t st = static_cast<hipStream_t>(stream);
     StepArgs* d_args = reinterpret_cast<StepArgs*>(ws + L.args);
     {
@@ -1448,19 +1551,6 @@ int lyk_hip_step_error(const void* d_workspace, int32_t* error_out, void* stream
     if (hipMemcpyAsync(error_out, d_workspace, 4, hipMemcpyDeviceToHost, st) != hipSuccess) return LYK_ERR_HIP;
     if (hipStreamSynchronize(st) != hipSuccess) return LYK_ERR_HIP;
     return LYK_OK;
-}
-
-void lyk_qkv_rope_order(int nq, int nkv, int hd, int32_t* perm) {
-    const int rows = (nq + 2 * nkv) * hd, half = hd / 2;
-    for (int pr = 0; pr < rows; ++pr) {
-        const int head = pr / hd, e = pr % hd;
-        int dim = e;
-        if (hd > 64) {
-            const int blk = e / 64, L = e % 64;
-            dim = L < 32 ? blk * 32 + L : half + blk * 32 + (L - 32);
-        }
-        perm[pr] = head * hd + dim;
-    }
 }
 
 }  // extern "C"

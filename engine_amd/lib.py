@@ -58,11 +58,11 @@ _KERNEL_SIGS = {
     "lyk_hip_gemv_q4": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
     "lyk_hip_gemv_q8": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
     "lyk_hip_step_workspace_bytes": (U64, [P, I]),
-    "lyk_hip_step_barriers": (U32, [P, I]),
+    "lyk_hip_step_phases": (U32, [P, I]),
+    "lyk_hip_step_grid": (I, []),
     "lyk_hip_decode_step": (I, [P, P, P, U64, I, P]),
     "lyk_hip_step_reset": (I, [P, U64, P]),
     "lyk_hip_step_error": (I, [P, C.POINTER(C.c_int32), P]),
-    "lyk_qkv_rope_order": (None, [I, I, I, P]),
 }
 
 class ModelConfig(C.Structure):

@@ -144,13 +144,17 @@ class HipModel:
     def set_step_tracing(self, on=True):
         L.check("lyk_model_set_step_tracing", L.model_lib().lyk_model_set_step_tracing(self._h, int(on)))
 
-    def step_trace(self):
-        """Device timestamps (100 MHz ticks) of the latest step: entry,
-        after each grid barrier, exit, then the arrivals at each barrier."""
-        n = 4 * (5 * self.cfg.num_layers + 1) + 2
+    def step_trace(self, mode="greedy"):
+        """Device timestamps (100 MHz ticks) of the latest step, per
+        workgroup: [grid][2 + 4*phases] = entry, exit, then per phase
+        (entered, inputs ready, main loop done, outputs written). `mode` is
+        the mode the buffer was sized for (the largest, greedy)."""
+        grid = L.kernels().lyk_hip_step_grid()
+        nph = 5 * self.cfg.num_layers + 2
+        n = grid * (4 * nph + 2)
         buf = (C.c_uint64 * n)()
         got = L.model_lib().lyk_model_step_trace(self._h, buf, n)
-        return list(buf)[:got]
+        return np.array(buf, dtype=np.int64)[:got]
 
 
 class Sequence:

@@ -216,13 +216,13 @@ int lyk_hip_argmax(const float* d_logits, int64_t ldl, int m, int64_t n,
  * the entry points above (same quantized formats, fp16 activations into each
  * GEMV, fp32 residual stream and softmax, fp16 KV cache).
  *
- * Weights: packed as above; qkv is one [(nq+2nkv)*hd, hidden] matrix in the
- * row order lyk_qkv_rope_order gives (bias in the same order), gate/up is a
- * paired packing (A = gate, B = up). The layer table is a device array. */
+ * Weights: packed as above; qkv is one [(nq+2nkv)*hd, hidden] matrix, rows
+ * [q | k | v] (bias the same), gate/up is a paired packing (A = gate,
+ * B = up). The layer table is a device array. */
 typedef struct lyk_step_layer {
     const void* qkv_w;
     const void* qkv_s;
-    const float* qkv_bias;  /* fp32 [(nq+2nkv)*hd], rope row order */
+    const float* qkv_bias;  /* fp32 [(nq+2nkv)*hd] */
     const void* o_w;
     const void* o_s;
     const void* gateup_w;
@@ -269,21 +269,23 @@ typedef struct lyk_step_io {
     int32_t* nonfinite;           /* GREEDY, optional: += non-finite logits */
     int32_t* history;             /* GREEDY, optional: history[*step] = token, */
     int32_t* step;                /*   ++*step (the GreedyRun chaining) */
-    uint64_t* trace;              /* optional, 4*barriers + 2 values: s_memrealtime
-                                     ticks (100 MHz) of workgroup 0 at entry [0],
-                                     leaving barrier i [1+i], at exit
-                                     [barriers+1], arriving at barrier i
-                                     [barriers+2+i], phase i's inputs ready
-                                     [2*barriers+2+i], its main loop done
-                                     [3*barriers+2+i] */
+    uint64_t* trace;              /* optional, grid * (4*phases + 2) values:
+                                     s_memrealtime ticks (100 MHz) per workgroup
+                                     w at [w*(4*phases+2) +]: entry [0], exit
+                                     [1]; phase i entered [2+4i], inputs ready
+                                     [3+4i], main loop done [4+4i], outputs
+                                     written [5+4i] */
 } lyk_step_io;
 
 /* Workspace for steps of up to max_rows rows (0 if the geometry is
  * unsupported). Prepare it with lyk_hip_step_reset before the first step;
  * afterwards every step leaves it valid for the next on the same stream. */
 uint64_t lyk_hip_step_workspace_bytes(const lyk_step_model* model, int max_rows);
-/* Grid barriers one step of `mode` performs. */
-uint32_t lyk_hip_step_barriers(const lyk_step_model* model, int mode);
+/* Phases one step of `mode` runs (per layer QKV, attention, O, gate/up,
+ * down; the LM head; the greedy argmax), and the workgroups of a launch:
+ * the trace holds lyk_hip_step_grid() * (4*phases + 2) values. */
+uint32_t lyk_hip_step_phases(const lyk_step_model* model, int mode);
+int lyk_hip_step_grid(void);
 /* Launches one step (stream-ordered, asynchronous). Positions must be
  * < rope_positions and have their blocks in the tables; the host checks
  * both. The launch arguments are kept in the workspace and uploaded only when
@@ -297,12 +299,6 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io,
 int lyk_hip_step_reset(void* d_workspace, uint64_t workspace_bytes, void* stream);
 /* Copies the error word (0 = no error) to *error_out and waits for it. */
 int lyk_hip_step_error(const void* d_workspace, int32_t* error_out, void* stream);
-/* Row order of the packed qkv matrix: packed row r holds natural row
- * perm[r] of [q | k | v]. Heads of hd > 64 are stored in blocks of 64 rows
- * that hold 32 RoPE pairs (dims d and d + hd/2 in rows j and j + 32);
- * smaller heads keep the natural order. */
-void lyk_qkv_rope_order(int nq, int nkv, int hd, int32_t* perm);
-
 int lyk_abi_version(void);
 
 #ifdef __cplusplus
