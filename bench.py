@@ -35,11 +35,6 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
 
 
-def qwen7b(max_context=32768):
-    from oracle.oracle import QwenConfig
-    return QwenConfig(152064, 3584, 28, 28, 4, 128, 18944, max_context, 1e-6, 1e6, False, 151643)
-
-
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -49,7 +44,7 @@ def run_decode(args):
     import torch
     from engine_amd import model as M
 
-    cfg = qwen7b()
+    cfg = M.QWEN25_7B
     t0 = time.time()
     opts = M.Options(quant=args.quant, kv_pool_tokens=args.prompt + args.warmup + args.steps + 512)
     hip = M.HipModel.synthetic(cfg, seed=0, sigma=0.02, options=opts)
@@ -105,10 +100,12 @@ def cpu_baseline(tokens=3):
     safetensors file (values do not change CPU time); the head is tied to the
     embedding, the same [152064, 3584] matvec as the untied 7B head."""
     from oracle import oracle as O
+    from engine_amd.model import QWEN25_7B
     import dataclasses
 
     use_ref = O.ref_available()
-    base = dataclasses.replace(qwen7b(64), tie_word_embeddings=True)
+    base = O.QwenConfig(**{**dataclasses.asdict(QWEN25_7B), "max_context_tokens": 64,
+                           "tie_word_embeddings": True})
     rng = np.random.default_rng(2)
     block = (rng.standard_normal(1 << 24).astype(np.float32) * 0.02)
     times = {}

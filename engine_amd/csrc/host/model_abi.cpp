@@ -45,6 +45,8 @@ HipModelOptions ToOptions(const lyk_model_options* o) {
     opt.kv_pool_tokens = o->kv_pool_tokens;
     if (o->kv_block_tokens) opt.kv_block_tokens = o->kv_block_tokens;
     opt.quantization = o->quant == 1 ? HipWeightQuant::kInt8 : HipWeightQuant::kInt4;
+    opt.attn_split_tokens = o->attn_split_tokens;
+    opt.attn_max_splits = o->attn_max_splits;
     return opt;
 }
 

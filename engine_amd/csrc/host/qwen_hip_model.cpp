@@ -700,6 +700,8 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
     md.rms_norm_eps = c.rms_norm_eps;
     md.block_tokens = int32_t(bt);
     md.num_blocks = int32_t(nblocks);
+    md.attn_split_tokens = options.attn_split_tokens;
+    md.attn_max_splits = options.attn_max_splits;
     md.embed = I.embed.as<float>();
     md.final_norm = I.final_norm.as<float>();
     md.lm_head_w = I.lm_head.qw.p;

@@ -39,6 +39,10 @@ struct HipModelOptions {
     uint32_t kv_pool_tokens = 0;
     uint32_t kv_block_tokens = 16;
     HipWeightQuant quantization = HipWeightQuant::kInt4;
+    // Attention context split over workgroups (tokens per split at least, a
+    // multiple of 16; splits at most, <= 32); 0 = the kernel's defaults.
+    int attn_split_tokens = 0;
+    int attn_max_splits = 0;
 };
 
 // fp32 weights by reference tensor name. The safetensors file is one source;

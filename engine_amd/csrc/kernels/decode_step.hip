@@ -31,8 +31,9 @@
 //     matrix has too few tiles for the grid (down projection) every tile's K
 //     range is cut into pieces; piece 0's workgroup adds the others' tagged
 //     partials in piece order. The activation vector sits in LDS.
-//   * Attention units are (row, kv head, context split); the O phase merges
-//     the splits in split order while filling its activations.
+//   * Attention units are (row, kv head, context split), q.k and p.v on the
+//     matrix cores; the splits of a kv head merge in split order, each split
+//     finishing a slice of the outputs.
 //   * Buffers are reused across layers; tags carry the layer, and every
 //     reader of a reused buffer produces data that the next writer of that
 //     buffer (a later layer) waits for, so no write overtakes a read. The
@@ -61,9 +62,8 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kPieces = 4;           // row tiles one wave's range may touch
 constexpr int kNormPer = 10;         // hidden_size <= kNormPer * kThreads
 constexpr int kMaxRows = 4;
-constexpr int kAttnMaxSplits = 12;   // context splits per (row, kv head)
-constexpr int kAttnSplitTokens = 128;
-constexpr int kPass = 64;            // attention tokens per pass (one per lane)
+constexpr int kAttnMaxSplits = 32;   // context splits per (row, kv head), at most
+constexpr int kAttnSplitTokens = 32; // default: tokens per split, at least
 constexpr int kMinPieceChunks = 4;   // K chunks per piece of a split tile, at least
 constexpr int kMaxPieces = 8;        // pieces per split tile, at most
 constexpr uint64_t kSpinTicks = 200000000ull;  // s_memrealtime is 100 MHz: 2 s
@@ -84,7 +84,8 @@ struct StepArgs {
     u64* dpart;           // [5][dpart_stride] split-tile partials [tiles][pieces][M][64] per GEMV kind
     size_t dpart_stride;
     u64* best;            // [M][head tiles][3] greedy candidates (value, index, non-finite)
-    int attn_split_tokens;  // context tokens per attention split, at least
+    int attn_split_tokens;  // context tokens per attention split, at least (multiple of 16)
+    int attn_max_splits;    // attention splits per (row, kv head), at most
     int phases;             // phases of one launch (trace layout)
 };
 
@@ -205,10 +206,10 @@ constexpr int chunk_k() { return Q8 ? 128 : 256; }
 // Pieces each row tile's K range is cut into: 1 unless the matrix has too
 // few tiles to give every workgroup work and each piece keeps at least
 // kMinPieceChunks chunks.
-__host__ __device__ __forceinline__ int tile_pieces(int64_t tiles, int64_t chunks, int G) {
+__host__ __device__ __forceinline__ int tile_pieces(int tiles, int chunks, int G) {
     if (tiles * 2 > G) return 1;
-    int64_t p = G / tiles;
-    const int64_t pmax = chunks / kMinPieceChunks;
+    int p = G / tiles;
+    const int pmax = chunks / kMinPieceChunks;
     if (p > pmax) p = pmax;
     if (p > kMaxPieces) p = kMaxPieces;
     return p < 1 ? 1 : (int)p;
@@ -216,9 +217,11 @@ __host__ __device__ __forceinline__ int tile_pieces(int64_t tiles, int64_t chunk
 
 // The workgroup's share of a phase: chunk range [f0, f1) of the flattened
 // (tile, chunk) space (whole tiles, or one piece of one tile) and the window
-// of K chunks it reads: LDS slot s holds chunk ca + s.
+// of K chunks it reads: LDS slot s holds chunk ca + s. 32-bit throughout: the
+// space has at most a few 10^5 chunks, and 64-bit division is a long
+// software sequence on the GPU.
 struct Part {
-    int64_t f0, f1;
+    int f0, f1;
     int pieces, gp;   // pieces per tile; workgroups with work
     int ca, win;
     bool busy;
@@ -231,8 +234,8 @@ __device__ __forceinline__ Part partition(const Mat& A) {
     if (p.pieces == 1) {
         p.gp = A.tiles < G ? A.tiles : G;
         p.busy = b < p.gp;
-        p.f0 = p.busy ? (int64_t)A.tiles * b / p.gp * A.chunks : 0;
-        p.f1 = p.busy ? (int64_t)A.tiles * (b + 1) / p.gp * A.chunks : 0;
+        p.f0 = p.busy ? A.tiles * b / p.gp * A.chunks : 0;
+        p.f1 = p.busy ? A.tiles * (b + 1) / p.gp * A.chunks : 0;
         p.ca = 0;
         p.win = A.chunks;
     } else {
@@ -240,8 +243,8 @@ __device__ __forceinline__ Part partition(const Mat& A) {
         p.busy = b < p.gp;
         const int t = b / p.pieces, s = b % p.pieces;
         const int c0 = A.chunks * s / p.pieces, c1 = A.chunks * (s + 1) / p.pieces;
-        p.f0 = p.busy ? (int64_t)t * A.chunks + c0 : 0;
-        p.f1 = p.busy ? (int64_t)t * A.chunks + c1 : 0;
+        p.f0 = p.busy ? t * A.chunks + c0 : 0;
+        p.f1 = p.busy ? t * A.chunks + c1 : 0;
         p.ca = c0;
         p.win = c1 - c0;
     }
@@ -255,7 +258,7 @@ struct ChunkMath;
 template <int M>
 struct ChunkMath<M, false> {
     static constexpr int CK = 256;
-    __device__ __forceinline__ static void load(const Mat& A, int64_t f, int lane, u32x4 (&w)[8], u32x4& s4) {
+    __device__ __forceinline__ static void load(const Mat& A, int f, int lane, u32x4 (&w)[8], u32x4& s4) {
         const LYK_GLOBAL u32x4* wt = gp(A.w + (size_t)f * 512 + lane);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -304,7 +307,7 @@ struct ChunkMath<M, false> {
 template <int M>
 struct ChunkMath<M, true> {
     static constexpr int CK = 128;
-    __device__ __forceinline__ static void load(const Mat& A, int64_t f, int lane, u32x4 (&w)[8], u32x4& s4) {
+    __device__ __forceinline__ static void load(const Mat& A, int f, int lane, u32x4 (&w)[8], u32x4& s4) {
         const LYK_GLOBAL u32x4* wt = gp(A.w + (size_t)f * 512 + lane);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -551,8 +554,8 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     const Part p = partition(A);
     const int b = blockIdx.x;
     const int lane = tid & 63, wave = uniform(tid >> 6);
-    const int64_t len = p.f1 - p.f0;
-    const int64_t w0 = p.f0 + len * wave / kWaves, w1 = p.f0 + len * (wave + 1) / kWaves;
+    const int len = p.f1 - p.f0;
+    const int w0 = p.f0 + len * wave / kWaves, w1 = p.f0 + len * (wave + 1) / kWaves;
 
     u32x4 wa[8], wb[8], sa, sb;
     if (w0 < w1) CM::load(A, w0, lane, wa, sa);
@@ -607,9 +610,9 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     asm("v_mov_b32 %0, %1" : "=v"(vmagic) : "s"(0x64006400u));
 
     if (w0 < w1) {
-        int64_t f = w0;
-        int c = (int)(f % A.chunks);
-        int t = (int)(f / A.chunks);
+        int f = w0;
+        int t = f / A.chunks;
+        int c = f - t * A.chunks;
         int q = 0;
         float acc[M];
 #pragma unroll
@@ -617,7 +620,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         // int8 per-row scale of the current tile
         float srow = 1.0f;
         if constexpr (Q8) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
-        const int cend = p.pieces == 1 ? A.chunks : (int)(p.f1 - (int64_t)t * A.chunks);
+        const int cend = p.pieces == 1 ? A.chunks : p.f1 - t * A.chunks;
         // One chunk: math on the buffer, then request the chunk two ahead
         // into it; a tile's sums go to its piece slot when the tile ends.
         auto step = [&](u32x4 (&wc)[8], u32x4& sc) -> bool {
@@ -650,19 +653,25 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     }
     __syncthreads();  // every wave is done with the x window
     mark(a, ph, 2);
+    // each wave's tile sums, and the tiles [first, last] its range touched
+    __shared__ int span[kWaves][2];
     {
-        const int64_t tf = w0 < w1 ? w0 / A.chunks : 0;
-        const int np = w0 < w1 ? (int)((w1 - 1) / A.chunks - tf + 1) : 0;
+        const int tf = w0 < w1 ? w0 / A.chunks : 0;
+        const int tl = w0 < w1 ? (w1 - 1) / A.chunks : -1;
+        if (lane == 0) {
+            span[wave][0] = tf;
+            span[wave][1] = tl;
+        }
 #pragma unroll
         for (int q = 0; q < kPieces; ++q)
-            if (q < np)
+            if (q <= tl - tf)
 #pragma unroll
                 for (int m = 0; m < M; ++m) red[((wave * kPieces + q) * M + m) * 64 + lane] = accq[q][m];
     }
     __syncthreads();
 
     // ---- finish the workgroup's tiles, one wave per tile
-    const int tA = (int)(p.f0 / A.chunks), tB = (int)((p.f1 - 1) / A.chunks);
+    const int tA = p.f0 / A.chunks, tB = (p.f1 - 1) / A.chunks;
     const bool greedy = a.io.mode == LYK_STEP_GREEDY;
     // a region per GEMV kind: the kinds of one layer share tags
     u64* dpart = a.dpart + (size_t)(kind == kQkv ? 0 : kind - 1) * a.dpart_stride;
@@ -672,9 +681,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
 #pragma unroll
         for (int m = 0; m < M; ++m) v[m] = 0.0f;
         for (int w = 0; w < kWaves; ++w) {
-            const int64_t a0 = p.f0 + len * w / kWaves, a1 = p.f0 + len * (w + 1) / kWaves;
-            if (a0 >= a1) continue;
-            const int tf = (int)(a0 / A.chunks), tl = (int)((a1 - 1) / A.chunks);
+            const int tf = span[w][0], tl = span[w][1];
             if (t < tf || t > tl) continue;
 #pragma unroll
             for (int m = 0; m < M; ++m) v[m] += red[((w * kPieces + (t - tf)) * M + m) * 64 + lane];
@@ -785,12 +792,21 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
 
 // ------------------------------------------------------------ attention
 
-// Context split of a row: splits of at least split_tokens tokens (a
-// multiple of the pass size), at most kAttnMaxSplits of them; a row's
-// arithmetic depends only on its own context length.
-__device__ __forceinline__ int split_size(int ctx, int split_tokens, int pass) {
-    int t = (ctx + kAttnMaxSplits - 1) / kAttnMaxSplits;
-    t = (t + pass - 1) / pass * pass;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileT = 16;                       // tokens per MFMA tile
+constexpr int kChunkT = 256;                     // tokens per softmax chunk (4 per lane)
+constexpr int kChunkTiles = kChunkT / kTileT;
+constexpr int kKTiles = kChunkTiles / kWaves;    // q.k tiles per wave per chunk
+
+// Context split of a row: equal runs of whole tiles, at least split_tokens
+// long, at most max_splits of them; a row's split depends only on its own
+// context length.
+__device__ __forceinline__ int split_size(int ctx, int split_tokens, int max_splits) {
+    int t = (ctx + max_splits - 1) / max_splits;
+    t = (t + kTileT - 1) / kTileT * kTileT;
     return t > split_tokens ? t : split_tokens;
 }
 
@@ -804,60 +820,81 @@ __device__ __forceinline__ float rot_hi(float a, float b, float c, float s) {
     return b * c + a * s;
 }
 
-// One attention unit per (row, kv head, context split); the G query heads of
-// the group share every K/V element it loads. A unit requests its first K/V
-// tile, then polls the raw q (and, for the unit that holds the current
-// position, k and v) sums of the QKV phase, adds the bias and applies RoPE
-// (the last unit also appends the row to the paged cache). Tokens go in
-// passes of kPass: the pass's K and V rows are staged in LDS (16-byte loads,
-// the next pass's requested before the current one is computed); scores run
-// one lane per token (wave h = head h), the online softmax per head in that
-// wave, and P.V one thread per (head, dim pair) output, so no cross-lane
-// reductions are needed. The last split of a row's kv head merges the
-// others' tagged partials, in split order, into the output.
+// fp32 x as two fp16 parts, hi + lo == x to ~22 bits: an fp16 MFMA of an
+// exact fp16 operand against both parts, accumulated in fp32, keeps the
+// fp32 operand's precision.
+__device__ __forceinline__ void split_f16(float x, uint16_t& hi, uint16_t& lo) {
+    hi = f2h(x);
+    lo = f2h(x - h2f(hi));
+}
+
+// Attention units are (row, kv head, context split); the G <= 16 query heads
+// of a kv head share every K/V element a unit loads, and both products run
+// on the matrix cores:
+//   * q.k: S^T[t][h] = K[t][:] . q[h][:] with v_mfma_f32_16x16x32_f16, A = a
+//     16-token K tile (each lane loads 16 bytes of one K row straight from
+//     the paged cache), B = the rotated queries split into fp16 high and low
+//     parts (two MFMAs), so the scores carry fp32 query precision. The result
+//     leaves lane l with head l%16 and tokens 4*(l/16)..+3 of the tile.
+//   * p.v: O[h][d] += P[h][t] V[t][d] with v_mfma_f32_16x16x16_f16; wave w
+//     owns head dims 16w..16w+15 over all of the unit's tokens. The V cache
+//     is stored transposed per block ([d][slot]), so the B operand, 4
+//     consecutive tokens of one dim, is one 8-byte load. P (split hi/lo like
+//     q) is read from LDS in exactly the layout q.k left it in.
+// Tokens run in chunks of up to 256: q.k of the chunk (tiles spread over the
+// waves) -> scores in LDS -> chunk max per head -> weights exp(s - max) and
+// their sum (one wave per head) -> p.v, the accumulator rescaled when the
+// running max grows. Each unit's K and V registers for the first chunk are
+// requested before it polls its inputs (the raw q, k, v sums of the QKV
+// phase, to which it adds the bias and applies RoPE); the unit holding the
+// current position appends its K row and V column to the cache and uses
+// them from LDS. With several splits, every unit writes its (max, sum,
+// unnormalised output) as tagged words; once a workgroup has computed all of
+// its units, each unit merges a 1/splits slice of its kv head's outputs over
+// the splits, in split order (no unit waits for a unit its own workgroup has
+// yet to compute).
 template <int M, int HD>
 __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const lyk_step_layer& Lw, uint32_t tag) {
-    const int tid = phase_tid();
-    constexpr int P = kPass;
-    constexpr int KS = HD + 2;                     // padded LDS row of K (halves): no bank conflicts
-    constexpr int CPR = HD / 8 > 0 ? HD / 8 : 1;   // 16-byte pieces per K/V row
-    constexpr int VB = HD % 8 == 0 ? 16 : HD * 2;  // bytes per piece
-    constexpr int kLoads = (P * CPR + kThreads - 1) / kThreads;
-    constexpr int kPairs = (16 * HD / 2 + kThreads - 1) / kThreads;  // (head, dim pair) per thread, G <= 16
+    constexpr int KS = (HD + 31) / 32;   // 32-dim steps of q.k
+    constexpr int DB = (HD + 15) / 16;   // 16-dim blocks of p.v, one per wave
+    constexpr int QS = KS * 32 + 8;      // LDS row of q (halves), padded against bank conflicts
+    constexpr int SS = kChunkT + 4;      // LDS row of scores (floats)
     constexpr int half = HD / 2;
-    using Piece = typename std::conditional<(VB == 16), u32x4,
-                                            typename std::conditional<(VB == 8), u64, uint32_t>::type>::type;
-    static_assert(HD % 8 == 0 || HD * 2 <= 16, "head dim");
+    static_assert(DB <= kWaves && (HD % 8 == 0 || HD == 4), "head dim");
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ float m_s[16], l_s[16], a_s[16];
-    __shared__ float ml_all[kAttnMaxSplits][16][2];
+    __shared__ float m_s[16], l_s[16], al_s[16], wmax[kWaves][16];
+    const int tid = phase_tid();
     mark(a, ph, 0);
     const int nq = a.md.num_heads, nkv = a.md.num_kv_heads;
     const int G = nq / nkv, bt = a.md.block_tokens;
     const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, quad = lane >> 4;   // MFMA column / row quad of this lane
     const float scale = 1.0f / sqrtf((float)HD);
     const int GH = G * HD;
-    float* q_s = reinterpret_cast<float*>(smem);                  // [G][HD] rotated queries
-    float* p_s = q_s + GH;                                         // [G][P] softmax weights
-    float* k_f = p_s + G * P;                                      // [HD] current key, fp32
-    uint16_t* ks = reinterpret_cast<uint16_t*>(k_f + HD);          // [P][KS] K tile
-    uint16_t* vs = ks + P * KS;                                    // [P][HD] V tile
-    uint16_t* kcur = vs + P * HD;                                  // [HD] current key, fp16
-    uint16_t* vcur = kcur + HD;                                    // [HD] current value, fp16
-    float* part = reinterpret_cast<float*>(smem);                  // [kAttnMaxSplits][GH] merge
+    uint16_t* qh = reinterpret_cast<uint16_t*>(smem);    // [16][QS] rotated q, fp16 high part
+    uint16_t* ql = qh + 16 * QS;                          // [16][QS] low part
+    uint16_t* wh = ql + 16 * QS;                          // [G][kChunkT] softmax weights, high
+    uint16_t* wl = wh + G * kChunkT;                      // low
+    uint16_t* kcur = wl + G * kChunkT;                    // [KS*32] current key (rotated), fp16
+    uint16_t* vcur = kcur + KS * 32;                      // [KS*32] current value, fp16
+    float* k_f = reinterpret_cast<float*>(vcur + KS * 32);  // [HD] current key, fp32
+    float* sc = k_f + (HD + 3) / 4 * 4;                   // [G][SS] chunk scores / raw q / merge
     const int kq = nq * HD, rows = (nq + 2 * nkv) * HD;
 
     int S[M], T[M], ctxs[M], units = 0;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         ctxs[m] = ld(a.io.positions + m) + 1;
-        T[m] = split_size(ctxs[m], a.attn_split_tokens, P);
+        T[m] = split_size(ctxs[m], a.attn_split_tokens, a.attn_max_splits);
         S[m] = (ctxs[m] + T[m] - 1) / T[m];
         units += nkv * S[m];
     }
-    bool ok = true;
-    for (int u = blockIdx.x; u < units; u += gridDim.x) {
-        int m = 0, r = u, Sm = S[0], Tm = T[0], ctx = ctxs[0];
+    auto unit_of = [&](int u, int& m, int& g, int& s, int& Sm, int& Tm, int& ctx) {
+        int r = u;
+        m = 0;
+        Sm = S[0];
+        Tm = T[0];
+        ctx = ctxs[0];
 #pragma unroll
         for (int mm = 1; mm < M; ++mm)
             if (m == mm - 1 && r >= nkv * Sm) {
@@ -867,7 +904,13 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 Tm = T[mm];
                 ctx = ctxs[mm];
             }
-        const int g = r / Sm, s = r % Sm;
+        g = r / Sm;
+        s = r % Sm;
+    };
+    bool ok = true;
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        int m, g, s, Sm, Tm, ctx;
+        unit_of(u, m, g, s, Sm, Tm, ctx);
         const int pos = ctx - 1;
         const int t0 = s * Tm, t1 = min(ctx, t0 + Tm);
         const bool last = s == Sm - 1;   // holds the current position
@@ -876,49 +919,79 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         const size_t blk_stride = (size_t)nkv * head_stride;
         const uint16_t* kc = Lw.k_cache + (size_t)g * head_stride;
         const uint16_t* vc = Lw.v_cache + (size_t)g * head_stride;
+        const int dv = wave * kTileT + col;   // this lane's dim in p.v
 
-        // this thread's pieces of the K/V rows of the pass at c0 (the
-        // current position's row comes from LDS when staged)
-        auto load_kv = [&](int c0, Piece (&kk)[kLoads], Piece (&vv)[kLoads]) {
+        // K rows of this wave's q.k tiles and V runs of its dims, for the
+        // chunk at c0 (zero past the split and at the current position). A
+        // tile never straddles a block (block_tokens is a multiple of 16):
+        // one block lookup per tile, with wave-uniform arithmetic.
+        u32x4 kr[kKTiles][KS];
+        u64 vr[kChunkTiles];
+        auto tile_block = [&](int tt, int& slot) -> size_t {   // tt: first token of a tile
+            const int tb = uniform(tt) / bt;
+            slot = uniform(tt) - tb * bt;
+            return (size_t)ld(tab + tb) * blk_stride;
+        };
+        auto load_k = [&](int c0) {
 #pragma unroll
-            for (int i = 0; i < kLoads; ++i) {
-                const int e = tid + i * kThreads, j = e / CPR, c = e % CPR;
-                const int t = c0 + j;
-                if (j < P && t < t1 && t != pos) {
-                    const size_t off = (size_t)ld(tab + t / bt) * blk_stride + (size_t)(t % bt) * HD + c * (VB / 2);
-                    kk[i] = ld(reinterpret_cast<const Piece*>(kc + off));
-                    vv[i] = ld(reinterpret_cast<const Piece*>(vc + off));
+            for (int i = 0; i < kKTiles; ++i) {
+                const int tt = c0 + (wave + i * kWaves) * kTileT, t = tt + col;
+                const bool live = t < t1 && t != pos;
+                size_t row = 0;
+                if (tt < t1) {
+                    int slot;
+                    row = tile_block(tt, slot) + (size_t)(slot + col) * HD;
+                }
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int d = ks * 32 + quad * 8;
+                    kr[i][ks] = u32x4{0u, 0u, 0u, 0u};
+                    if (live && d < HD) {
+                        if constexpr (HD % 8 == 0) {
+                            kr[i][ks] = ld(reinterpret_cast<const u32x4*>(kc + row + d));
+                        } else {
+                            const u64 w = ld(reinterpret_cast<const u64*>(kc + row + d));
+                            kr[i][ks].x = (uint32_t)w;
+                            kr[i][ks].y = (uint32_t)(w >> 32);
+                        }
+                    }
                 }
             }
         };
-        auto stage = [&](int c0, const Piece (&kk)[kLoads], const Piece (&vv)[kLoads]) {
+        auto load_v = [&](int c0) {
 #pragma unroll
-            for (int i = 0; i < kLoads; ++i) {
-                const int e = tid + i * kThreads, j = e / CPR, c = e % CPR;
-                const int t = c0 + j;
-                if (j < P && t < t1) {
-                    Piece kp = kk[i], vp = vv[i];
-                    if (t == pos) {
-                        __builtin_memcpy(&kp, kcur + c * (VB / 2), VB);
-                        __builtin_memcpy(&vp, vcur + c * (VB / 2), VB);
-                    }
-                    uint32_t kw[VB / 4], vw[VB / 4];
-                    __builtin_memcpy(kw, &kp, VB);
-                    __builtin_memcpy(vw, &vp, VB);
-                    uint32_t* kd = reinterpret_cast<uint32_t*>(ks + j * KS + c * (VB / 2));
-                    uint32_t* vd = reinterpret_cast<uint32_t*>(vs + j * HD + c * (VB / 2));
-#pragma unroll
-                    for (int w = 0; w < VB / 4; ++w) {
-                        kd[w] = kw[w];
-                        vd[w] = vw[w];
+            for (int j = 0; j < kChunkTiles; ++j) {
+                const int tt = c0 + j * kTileT, r0 = tt + quad * 4;   // r0: first of the lane's 4 tokens
+                vr[j] = 0;
+                if (wave < DB && tt < t1) {
+                    int slot;
+                    const size_t bo = tile_block(tt, slot);
+                    if (dv < HD && r0 < t1) {
+                        u64 w = ld(reinterpret_cast<const u64*>(vc + bo + (size_t)dv * bt + slot + quad * 4));
+                        const int valid = t1 - r0;
+                        if (valid < 4) w &= (1ull << (16 * valid)) - 1;
+                        vr[j] = w;
                     }
                 }
             }
         };
-        Piece ka[kLoads], va[kLoads];
-        load_kv(t0, ka, va);
+        load_k(t0);
+        load_v(t0);
+        // zero what the MFMA operands read but RoPE does not write: q rows of
+        // absent heads, dims past the head dim
+        for (int e = tid; e < 16 * QS; e += kThreads) {
+            const int h = e / QS, d = e % QS;
+            if (h >= G || d >= HD) qh[e] = ql[e] = 0;
+        }
+        for (int e = tid; e < 2 * KS * 32; e += kThreads)
+            if (e % (KS * 32) >= HD) kcur[e] = 0;
 
+        // this thread's RoPE factors (its dim i = tid % (HD/2) in every
+        // pass, HD/2 dividing the block), requested before the inputs
+        const float rc = ld(a.md.rope_cos + (size_t)pos * half + tid % half);
+        const float rs = ld(a.md.rope_sin + (size_t)pos * half + tid % half);
         // raw q (and current k, v) sums + bias, polled
+        float* q_f = sc;   // [G][HD]
         const u64* src = a.qkv + (size_t)m * rows;
         {
             const int nw = GH + (last ? 2 * HD : 0);
@@ -926,10 +999,13 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 uint32_t v[4];
                 uint32_t have = 0;
                 int idx[4];
+                float bias[4];
 #pragma unroll
                 for (int u2 = 0; u2 < 4; ++u2) {
                     const int e = e0 + u2 * kThreads;
-                    idx[u2] = e < GH ? g * GH + e : (e < GH + HD ? kq + g * HD + (e - GH) : kq + nkv * HD + g * HD + (e - GH - HD));
+                    idx[u2] = e < GH ? g * GH + e
+                                     : (e < GH + HD ? kq + g * HD + (e - GH) : kq + nkv * HD + g * HD + (e - GH - HD));
+                    bias[u2] = e < nw ? ld(Lw.qkv_bias + idx[u2]) : 0.0f;
                 }
                 auto pending = [&]() {
                     int missing = 0;
@@ -947,209 +1023,237 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 for (int u2 = 0; u2 < 4; ++u2) {
                     const int e = e0 + u2 * kThreads;
                     if (e >= nw) continue;
-                    const float x = bitsf(v[u2]) + ld(Lw.qkv_bias + idx[u2]);
-                    if (e < GH) q_s[e] = x;
+                    const float x = bitsf(v[u2]) + bias[u2];
+                    if (e < GH) q_f[e] = x;
                     else if (e < GH + HD) k_f[e - GH] = x;
                     else vcur[e - GH - HD] = f2h(x);
                 }
             }
         }
         if (__syncthreads_or(!ok)) return false;
-        // RoPE on q (every head) and on the current key, from the host-built
-        // cos/sin tables; the current row goes to the paged cache
+        // RoPE on q (every head, split into fp16 parts) and on the current
+        // key, from the host-built cos/sin tables
         {
-            const float* cs = a.md.rope_cos + (size_t)pos * half;
-            const float* sn = a.md.rope_sin + (size_t)pos * half;
+            static_assert(kThreads % (HD / 2) == 0, "RoPE dims per thread");
             for (int e = tid; e < (G + (last ? 1 : 0)) * half; e += kThreads) {
                 const int h = e / half, i = e % half;
-                const float c = ld(cs + i), sv = ld(sn + i);
-                float* base = h < G ? q_s + h * HD : k_f;
+                const float* base = h < G ? q_f + h * HD : k_f;
                 const float lo = base[i], hi = base[i + half];
-                const float rl = rot_lo(lo, hi, c, sv), rh = rot_hi(lo, hi, c, sv);
+                const float rl = rot_lo(lo, hi, rc, rs), rh = rot_hi(lo, hi, rc, rs);
                 if (h < G) {
-                    base[i] = rl;
-                    base[i + half] = rh;
+                    split_f16(rl, qh[h * QS + i], ql[h * QS + i]);
+                    split_f16(rh, qh[h * QS + i + half], ql[h * QS + i + half]);
                 } else {
                     kcur[i] = f2h(rl);
                     kcur[i + half] = f2h(rh);
                 }
             }
         }
-        if (tid < 16) { m_s[tid] = -INFINITY; l_s[tid] = 0.0f; }
+        if (tid < 16) {
+            m_s[tid] = -INFINITY;
+            l_s[tid] = 0.0f;
+        }
         __syncthreads();
         if (last) {
+            // the current row into the cache: K row-major, V transposed
             const int blk = ld(tab + pos / bt);
-            const size_t off = (size_t)blk * blk_stride + (size_t)g * head_stride + (size_t)(pos % bt) * HD;
+            const size_t base = (size_t)blk * blk_stride + (size_t)g * head_stride;
             for (int i = tid; i < HD; i += kThreads) {
-                store_sc1_u16(Lw.k_cache + off + i, kcur[i]);
-                store_sc1_u16(Lw.v_cache + off + i, vcur[i]);
+                store_sc1_u16(Lw.k_cache + base + (size_t)(pos % bt) * HD + i, kcur[i]);
+                store_sc1_u16(Lw.v_cache + base + (size_t)i * bt + pos % bt, vcur[i]);
             }
         }
         if (u == (int)blockIdx.x) mark(a, ph, 1);
 
-        float acc[kPairs][2];
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};   // O[4*quad + j][dv]
+        const int nch = (t1 - t0 + kChunkT - 1) / kChunkT;
+        for (int c = 0; c < nch; ++c) {
+            const int c0 = t0 + c * kChunkT;
+            const int n = min(kChunkT, t1 - c0);
+            // q.k of this wave's tiles -> scores; the wave's max per head
+            float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < kPairs; ++i) acc[i][0] = acc[i][1] = 0.0f;
-        for (int c0 = t0; c0 < t1; c0 += P) {
-            const int n = min(P, t1 - c0);
-            stage(c0, ka, va);
+            for (int i = 0; i < kKTiles; ++i) {
+                const int tl = wave + i * kWaves;
+                if (tl * kTileT < n) {
+                    const int t = c0 + tl * kTileT + col;   // the K row this lane supplies
+                    f32x4 sv = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        u32x4 kv = kr[i][ks];
+                        if (t == pos) kv = *reinterpret_cast<const u32x4*>(kcur + ks * 32 + quad * 8);
+                        const u32x4 qa = *reinterpret_cast<const u32x4*>(qh + col * QS + ks * 32 + quad * 8);
+                        const u32x4 qb = *reinterpret_cast<const u32x4*>(ql + col * QS + ks * 32 + quad * 8);
+                        const f16x8 kf = __builtin_bit_cast(f16x8, kv);
+                        sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, __builtin_bit_cast(f16x8, qa), sv, 0, 0, 0);
+                        sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, __builtin_bit_cast(f16x8, qb), sv, 0, 0, 0);
+                    }
+                    // this lane: head col, chunk tokens tl*16 + 4*quad + j
+                    const int tt = tl * kTileT + quad * 4;
+                    float o[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        o[j] = tt + j < n ? sv[j] * scale : -INFINITY;
+                        mx = fmaxf(mx, o[j]);
+                    }
+                    if (col < G) {
+                        float* d = sc + col * SS + tt;
+                        d[0] = o[0];
+                        d[1] = o[1];
+                        d[2] = o[2];
+                        d[3] = o[3];
+                    }
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            if (lane < 16) wmax[wave][lane] = mx;
+            if (c + 1 < nch) load_k(c0 + kChunkT);   // next chunk, in flight meanwhile
             __syncthreads();
-            if (c0 + P < t1) load_kv(c0 + P, ka, va);   // next pass, in flight meanwhile
-            // scores, one lane per token; then the online softmax of head h
+            if (tid < G) {
+                float cm = wmax[0][tid];
+#pragma unroll
+                for (int w = 1; w < kWaves; ++w) cm = fmaxf(cm, wmax[w][tid]);
+                const float mold = m_s[tid], mnew = fmaxf(mold, cm);
+                al_s[tid] = expf(mold - mnew);   // 0 on the first chunk
+                m_s[tid] = mnew;
+            }
+            __syncthreads();
+            // weights of head h (wave h), 4 tokens per lane, and their sum
             for (int h = wave; h < G; h += kWaves) {
-                float sc = -INFINITY;
-                if (lane < n) {
-                    const float* qh = q_s + h * HD;
-                    const uint16_t* kr = ks + lane * KS;
-                    float d0 = 0.0f, d1 = 0.0f;
+                const int tt = lane * 4;
+                float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (tt < n) {
+                    const float mh = m_s[h];
 #pragma unroll
-                    for (int d = 0; d < HD; d += 2) {
-                        const half2_t k2 = as_half2(*reinterpret_cast<const uint32_t*>(kr + d));
-                        d0 = fmaf(qh[d], (float)k2.x, d0);
-                        d1 = fmaf(qh[d + 1], (float)k2.y, d1);
-                    }
-                    sc = (d0 + d1) * scale;
+                    for (int j = 0; j < 4; ++j)
+                        if (tt + j < n) p[j] = expf(sc[h * SS + tt + j] - mh);
                 }
-                const float mx = wave_max(sc);
-                const float mold = m_s[h];
-                const float mnew = fmaxf(mold, mx);
-                const float pv = lane < n ? expf(sc - mnew) : 0.0f;
-                const float sum = wave_sum(pv);
-                p_s[h * P + lane] = pv;
-                if (lane == 0) {
-                    const float alpha = expf(mold - mnew);  // 0 on the first pass
-                    a_s[h] = alpha;
-                    l_s[h] = l_s[h] * alpha + sum;
-                    m_s[h] = mnew;
+                const float sum = wave_sum((p[0] + p[1]) + (p[2] + p[3]));
+                uint16_t hi[4], lo[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) split_f16(p[j], hi[j], lo[j]);
+                uint16_t* dh = wh + h * kChunkT + tt;
+                uint16_t* dl = wl + h * kChunkT + tt;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    dh[j] = hi[j];
+                    dl[j] = lo[j];
                 }
+                if (lane == 0) l_s[h] = l_s[h] * al_s[h] + sum;
             }
             __syncthreads();
-            // acc = alpha * acc + sum_t p[h][t] V[t][d pair]
+            // p.v over the chunk's tiles for this wave's dims
+            if (wave < DB) {
 #pragma unroll
-            for (int i = 0; i < kPairs; ++i) {
-                const int e = tid + i * kThreads;     // (head, dim pair)
-                if (e < GH / 2) {
-                    const int h = e / half, dp = e % half;
-                    const float al = a_s[h];
-                    float x0 = acc[i][0] * al, x1 = acc[i][1] * al;
-                    const float* ph_ = p_s + h * P;
-                    const uint16_t* vcol = vs + dp * 2;
-                    for (int t = 0; t < n; ++t) {
-                        const half2_t v2 = as_half2(*reinterpret_cast<const uint32_t*>(vcol + t * HD));
-                        x0 = fmaf(ph_[t], (float)v2.x, x0);
-                        x1 = fmaf(ph_[t], (float)v2.y, x1);
-                    }
-                    acc[i][0] = x0;
-                    acc[i][1] = x1;
+                for (int j = 0; j < 4; ++j) {
+                    const int h = quad * 4 + j;
+                    acc[j] *= h < G ? al_s[h] : 0.0f;
                 }
+                const int ntl = (n + kTileT - 1) / kTileT;
+#pragma unroll
+                for (int j = 0; j < kChunkTiles; ++j) {
+                    if (j < ntl) {
+                        u64 vw = vr[j];
+                        const int r0 = c0 + j * kTileT + quad * 4;
+                        if (pos >= r0 && pos < r0 + 4) {
+                            const int sh = 16 * (pos - r0);
+                            vw = (vw & ~(0xffffull << sh)) | ((u64)vcur[dv] << sh);
+                        }
+                        u64 pa = 0, pb = 0;
+                        if (col < G) {
+                            pa = *reinterpret_cast<const u64*>(wh + col * kChunkT + j * kTileT + quad * 4);
+                            pb = *reinterpret_cast<const u64*>(wl + col * kChunkT + j * kTileT + quad * 4);
+                        }
+                        const f16x4 vf = __builtin_bit_cast(f16x4, vw);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pa), vf, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, pb), vf, acc, 0, 0, 0);
+                    }
+                }
+                if (c + 1 < nch) load_v(c0 + kChunkT);
             }
-            __syncthreads();  // the tiles and p_s are rewritten by the next pass
+            __syncthreads();   // scores and weights are rewritten by the next chunk
         }
         if (u == (int)blockIdx.x) mark(a, ph, 2);
         const size_t grp = (size_t)m * nkv + g;
-        u64* out = a.attn_out + (size_t)m * kq + (size_t)g * GH;
-        if (!last) {
-            // a partial for the row's last split to merge
-            u64* ml = a.attn_ml + (grp * kAttnMaxSplits + s) * G * 2;
+        if (wave < DB && dv < HD) {
+            u64* out = a.attn_out + (size_t)m * kq + (size_t)g * GH;
             u64* pa = a.attn_acc + (grp * kAttnMaxSplits + s) * (size_t)GH;
-            if (tid < G) {
-                put(&ml[2 * tid], fbits(m_s[tid]), tag);
-                put(&ml[2 * tid + 1], fbits(l_s[tid]), tag);
-            }
 #pragma unroll
-            for (int i = 0; i < kPairs; ++i) {
-                const int e = tid + i * kThreads;
-                if (e < GH / 2) {
-                    put(&pa[2 * e], fbits(acc[i][0]), tag);
-                    put(&pa[2 * e + 1], fbits(acc[i][1]), tag);
+            for (int j = 0; j < 4; ++j) {
+                const int h = quad * 4 + j;
+                if (h < G) {
+                    if (Sm == 1) put(&out[h * HD + dv], fbits(acc[j] / l_s[h]), tag);
+                    else put(&pa[h * HD + dv], fbits(acc[j]), tag);
                 }
             }
-        } else if (Sm == 1) {
-#pragma unroll
-            for (int i = 0; i < kPairs; ++i) {
-                const int e = tid + i * kThreads;
-                if (e < GH / 2) {
-                    const float l = l_s[e / half];
-                    put(&out[2 * e], fbits(acc[i][0] / l), tag);
-                    put(&out[2 * e + 1], fbits(acc[i][1] / l), tag);
-                }
-            }
-        } else {
-            // merge splits 0..S-1 in order: out = sum e_s acc_s / sum e_s l_s
-            if (tid < G) {
-                ml_all[Sm - 1][tid][0] = m_s[tid];
-                ml_all[Sm - 1][tid][1] = l_s[tid];
-            }
-            for (int e0 = tid; e0 < (Sm - 1) * (GH + 2 * G); e0 += kThreads * 4) {
-                uint32_t v[4];
-                uint32_t have = 0;
-                auto where = [&](int e, const u64*& w, float*& dst) {
-                    const int sp = e / (GH + 2 * G), rr = e % (GH + 2 * G);
-                    if (rr < GH) {
-                        w = a.attn_acc + (grp * kAttnMaxSplits + sp) * (size_t)GH + rr;
-                        dst = part + (size_t)sp * GH + rr;
-                    } else {
-                        const int k2 = rr - GH;
-                        w = a.attn_ml + (grp * kAttnMaxSplits + sp) * G * 2 + k2;
-                        dst = &ml_all[sp][k2 / 2][k2 % 2];
-                    }
-                };
-                auto pending = [&]() {
-                    int missing = 0;
-#pragma unroll
-                    for (int u2 = 0; u2 < 4; ++u2) {
-                        const int e = e0 + u2 * kThreads;
-                        if (e >= (Sm - 1) * (GH + 2 * G) || (have >> u2 & 1)) continue;
-                        const u64* w;
-                        float* dst;
-                        where(e, w, dst);
-                        if (take(w, tag, v[u2])) have |= 1u << u2;
-                        else ++missing;
-                    }
-                    return missing;
-                };
-                ok = spin(a, pending) && ok;
+        }
+        if (Sm > 1 && tid < G) {
+            u64* ml = a.attn_ml + (grp * kAttnMaxSplits + s) * G * 2;
+            put(&ml[2 * tid], fbits(m_s[tid]), tag);
+            put(&ml[2 * tid + 1], fbits(l_s[tid]), tag);
+        }
+        __syncthreads();   // LDS is rewritten by the next unit
+    }
+
+    // merge: unit s of a split kv head finishes outputs [s*E, (s+1)*E) of
+    // its G*HD: out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max)
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        int m, g, s, Sm, Tm, ctx;
+        unit_of(u, m, g, s, Sm, Tm, ctx);
+        if (Sm == 1) continue;
+        const size_t grp = (size_t)m * nkv + g;
+        const int E = (GH + Sm - 1) / Sm, e0 = s * E, ne = max(0, min(GH, e0 + E) - e0);
+        float* mlv = sc;                                // [Sm][G][2] max, sum -> weight, sum
+        float* vals = sc + kAttnMaxSplits * 16 * 2;     // [ne][Sm]
+        __shared__ float lsum[16];
+        const int nml = Sm * G * 2, nw = nml + ne * Sm;
+        for (int b0 = tid; b0 < nw; b0 += kThreads * 4) {
+            uint32_t v[4];
+            uint32_t have = 0;
+            auto word = [&](int e) -> const u64* {
+                if (e < nml) return a.attn_ml + (grp * kAttnMaxSplits + e / (2 * G)) * G * 2 + e % (2 * G);
+                const int k = e - nml;
+                return a.attn_acc + (grp * kAttnMaxSplits + k % Sm) * (size_t)GH + e0 + k / Sm;
+            };
+            auto pending = [&]() {
+                int missing = 0;
 #pragma unroll
                 for (int u2 = 0; u2 < 4; ++u2) {
-                    const int e = e0 + u2 * kThreads;
-                    if (e >= (Sm - 1) * (GH + 2 * G)) continue;
-                    const u64* w;
-                    float* dst;
-                    where(e, w, dst);
-                    *dst = bitsf(v[u2]);
+                    const int e = b0 + u2 * kThreads;
+                    if (e >= nw || (have >> u2 & 1)) continue;
+                    if (take(word(e), tag, v[u2])) have |= 1u << u2;
+                    else ++missing;
                 }
-            }
-            if (__syncthreads_or(!ok)) return false;
-            if (tid < G) {
-                float mx = -INFINITY;
-                for (int sp = 0; sp < Sm; ++sp) mx = fmaxf(mx, ml_all[sp][tid][0]);
-                float L = 0.0f;
-                for (int sp = 0; sp < Sm; ++sp) {
-                    const float es = expf(ml_all[sp][tid][0] - mx);
-                    ml_all[sp][tid][0] = es;
-                    L += ml_all[sp][tid][1] * es;
-                }
-                l_s[tid] = L;
-            }
-            __syncthreads();
+                return missing;
+            };
+            ok = spin(a, pending) && ok;
 #pragma unroll
-            for (int i = 0; i < kPairs; ++i) {
-                const int e = tid + i * kThreads;
-                if (e < GH / 2) {
-                    const int h = e / half;
-                    float o0 = 0.0f, o1 = 0.0f;
-                    for (int sp = 0; sp < Sm - 1; ++sp) {
-                        const float w = ml_all[sp][h][0];
-                        o0 += part[(size_t)sp * GH + 2 * e] * w;
-                        o1 += part[(size_t)sp * GH + 2 * e + 1] * w;
-                    }
-                    const float w = ml_all[Sm - 1][h][0];
-                    o0 += acc[i][0] * w;
-                    o1 += acc[i][1] * w;
-                    put(&out[2 * e], fbits(o0 / l_s[h]), tag);
-                    put(&out[2 * e + 1], fbits(o1 / l_s[h]), tag);
-                }
+            for (int u2 = 0; u2 < 4; ++u2) {
+                const int e = b0 + u2 * kThreads;
+                if (e < nml) mlv[e] = bitsf(v[u2]);
+                else if (e < nw) vals[e - nml] = bitsf(v[u2]);
             }
+        }
+        if (__syncthreads_or(!ok)) return false;
+        if (tid < G) {
+            float mx = -INFINITY;
+            for (int sp = 0; sp < Sm; ++sp) mx = fmaxf(mx, mlv[(sp * G + tid) * 2]);
+            float L = 0.0f;
+            for (int sp = 0; sp < Sm; ++sp) {
+                const float es = expf(mlv[(sp * G + tid) * 2] - mx);
+                mlv[(sp * G + tid) * 2] = es;
+                L += mlv[(sp * G + tid) * 2 + 1] * es;
+            }
+            lsum[tid] = L;
+        }
+        __syncthreads();
+        u64* out = a.attn_out + (size_t)m * kq + (size_t)g * GH;
+        for (int k = tid; k < ne; k += kThreads) {
+            const int h = (e0 + k) / HD;
+            float o = 0.0f;
+            for (int sp = 0; sp < Sm; ++sp) o += vals[k * Sm + sp] * mlv[(sp * G + h) * 2];
+            put(&out[e0 + k], fbits(o / lsum[h]), tag);
         }
         __syncthreads();   // LDS is rewritten by the next unit
     }
@@ -1267,7 +1371,6 @@ int chunks_of(int64_t k, bool q8) {
     return (int)(((k + unit - 1) / unit + 7) / 8);
 }
 
-int vec_of(int hd) { return hd % 8 == 0 ? 8 : 2; }
 
 // Head dims with a compiled attention path.
 bool head_dim_supported(int hd) { return hd == 4 || hd == 64 || hd == 128; }
@@ -1295,9 +1398,10 @@ int check_model(const lyk_step_model& md) {
     const int hd = md.head_dim;
     if (md.num_heads % md.num_kv_heads) return LYK_ERR_INVALID_ARG;
     const int G = md.num_heads / md.num_kv_heads;
-    const int vec = vec_of(hd);
-    if (!head_dim_supported(hd)) return LYK_ERR_SHAPE;
-    if (G > (64 / vec < 16 ? 64 / vec : 16)) return LYK_ERR_SHAPE;
+    if (!head_dim_supported(hd) || G > 16 || md.block_tokens % 16) return LYK_ERR_SHAPE;
+    if (md.attn_split_tokens < 0 || md.attn_split_tokens % 16 || md.attn_max_splits < 0 ||
+        md.attn_max_splits > kAttnMaxSplits)
+        return LYK_ERR_INVALID_ARG;
     if (md.hidden_size > kNormPer * kThreads || (md.intermediate_size & 1) || md.num_layers > 255)
         return LYK_ERR_SHAPE;
     return LYK_OK;
@@ -1391,9 +1495,14 @@ size_t lds_bytes(const lyk_step_model& md, int rows, int grid) {
         const PhaseShape ps = phase_shape(mt, q8, grid);
         need = std::max(need, (size_t)rows * ps.win * ck * 2);
     }
-    const size_t G = md.num_heads / md.num_kv_heads, hd = md.head_dim, P = kPass;
-    need = std::max(need, (G * hd + G * P + hd) * 4 + (P * (hd + 2) + P * hd + 2 * hd) * 2);
-    need = std::max(need, (size_t)kAttnMaxSplits * G * hd * 4);
+    // attention: q high/low parts, chunk weights high/low, current k and v
+    // (fp16), current k (fp32), then the larger of the chunk scores, the raw
+    // q and the merge's (max, sum) table + partial slice
+    const size_t G = md.num_heads / md.num_kv_heads, hd = md.head_dim;
+    const size_t KS = (hd + 31) / 32, QS = KS * 32 + 8;
+    const size_t front = 2 * 16 * QS * 2 + 2 * G * kChunkT * 2 + 2 * KS * 32 * 2 + (hd + 3) / 4 * 4 * 4;
+    const size_t tail = std::max({G * (kChunkT + 4), G * hd, (size_t)kAttnMaxSplits * 16 * 2 + G * hd + kAttnMaxSplits});
+    need = std::max(need, front + tail * 4);
     return need;
 }
 
@@ -1464,7 +1573,7 @@ extern "C" {
 uint64_t lyk_hip_step_workspace_bytes(const lyk_step_model* model, int max_rows) {
     if (!model || max_rows < 1 || max_rows > kMaxRows || check_model(*model) != LYK_OK) return 0;
     const int grid = step_grid();
-    if (grid < kAttnMaxSplits || !pieces_ok(*model, grid)) return 0;
+    if (!pieces_ok(*model, grid)) return 0;
     if (lds_bytes(*model, max_rows, grid) > kMaxDynamicLds) return 0;
     return layout(*model, max_rows, grid).total;
 }
@@ -1492,7 +1601,7 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     if (io->mode == LYK_STEP_GREEDY && m != 1) return LYK_ERR_INVALID_ARG;
     const int grid = step_grid();
     if (grid < 1) return LYK_ERR_HIP;
-    if (grid < kAttnMaxSplits || !pieces_ok(*model, grid)) return LYK_ERR_SHAPE;
+    if (!pieces_ok(*model, grid)) return LYK_ERR_SHAPE;
     const Layout L = layout(*model, max_rows, grid);
     if (L.total > workspace_bytes) return LYK_ERR_WORKSPACE;
     const size_t lds = lds_bytes(*model, m, grid);
@@ -1515,7 +1624,8 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     a.dpart = reinterpret_cast<u64*>(ws + L.dpart);
     a.dpart_stride = (size_t)L.dpart_stride;
     a.best = reinterpret_cast<u64*>(ws + L.best);
-    a.attn_split_tokens = kAttnSplitTokens;
+    a.attn_split_tokens = model->attn_split_tokens ? model->attn_split_tokens : kAttnSplitTokens;
+    a.attn_max_splits = model->attn_max_splits ? model->attn_max_splits : kAttnMaxSplits;
     a.phases = (int)lyk_hip_step_phases(model, io->mode);
     hipStream_t st = static_cast<hipStream_t>(stream);
     StepArgs* d_args = reinterpret_cast<StepArgs*>(ws + L.args);

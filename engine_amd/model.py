@@ -28,6 +28,29 @@ def _p(a):
     return a.ctypes.data_as(C.c_void_p)
 
 
+@dataclass
+class QwenConfig:
+    """Qwen2 dense decoder shape; model/architectures/qwen/qwen_model.h:22-37
+    (one eos id here: the hip model consults none on device)."""
+    vocab_size: int
+    hidden_size: int
+    num_layers: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    intermediate_size: int
+    max_context_tokens: int
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 10000.0
+    tie_word_embeddings: bool = True
+    eos_token_id: int = 0
+
+
+# Qwen2.5-7B (config.json of the released checkpoint): 28 layers, 28 query and
+# 4 KV heads of 128, SwiGLU 18944, vocab 152064, untied LM head.
+QWEN25_7B = QwenConfig(152064, 3584, 28, 28, 4, 128, 18944, 32768, 1e-6, 1e6, False, 151643)
+
+
 def _config(cfg):
     return L.ModelConfig(cfg.vocab_size, cfg.hidden_size, cfg.num_layers, cfg.num_heads,
                          cfg.num_kv_heads, cfg.head_dim, cfg.intermediate_size,
@@ -41,10 +64,13 @@ class Options:
     kv_pool_tokens: int = 0
     kv_block_tokens: int = 16
     quant: str = "int4"
+    attn_split_tokens: int = 0   # 0: the kernel's defaults
+    attn_max_splits: int = 0
 
     def c(self):
         return L.ModelOptions(self.device_id, self.kv_pool_tokens, self.kv_block_tokens,
-                              1 if self.quant == "int8" else 0)
+                              1 if self.quant == "int8" else 0, self.attn_split_tokens,
+                              self.attn_max_splits)
 
 
 class HipModel:

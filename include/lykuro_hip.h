@@ -232,7 +232,10 @@ typedef struct lyk_step_layer {
     const float* input_norm;
     const float* post_norm;
     uint16_t* k_cache;      /* fp16 [num_blocks][nkv][block_tokens][hd] */
-    uint16_t* v_cache;
+    uint16_t* v_cache;      /* fp16 [num_blocks][nkv][hd][block_tokens]: V is
+                               stored transposed within each block, so runs of
+                               consecutive tokens of one dim are contiguous (the
+                               operand layout of the p.v matrix product) */
 } lyk_step_layer;
 
 typedef struct lyk_step_model {
@@ -240,8 +243,12 @@ typedef struct lyk_step_model {
         intermediate_size;
     int32_t q8;              /* 0: int4 weights, 1: int8 weights */
     float rms_norm_eps;
-    int32_t block_tokens, num_blocks;
+    int32_t block_tokens, num_blocks;  /* block_tokens: a multiple of 16 */
     int32_t rope_positions;  /* rows of the cos/sin tables */
+    /* Attention split of a row's context over workgroups: equal splits of
+     * whole 16-token tiles, at least attn_split_tokens (a multiple of 16) long,
+     * at most attn_max_splits (<= 32) of them; 0 selects the defaults (32, 32). */
+    int32_t attn_split_tokens, attn_max_splits;
     const float* embed;      /* fp32 [vocab][hidden] */
     const float* final_norm;
     const void* lm_head_w;

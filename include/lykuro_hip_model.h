@@ -36,8 +36,11 @@ typedef struct lyk_model_config {
 typedef struct lyk_model_options {
     int32_t device_id;
     uint32_t kv_pool_tokens;
-    uint32_t kv_block_tokens;
+    uint32_t kv_block_tokens;  /* a multiple of 16 */
     int32_t quant;
+    /* attention context split (lyk_step_model fields of the same names);
+     * 0 selects the defaults */
+    int32_t attn_split_tokens, attn_max_splits;
 } lyk_model_options;
 
 /* QwenHipModel::Load from a safetensors file (replaces QwenCudaModel::Load,

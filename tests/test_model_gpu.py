@@ -256,3 +256,102 @@ def test_synthetic_model_greedy_32_steps(cuda, cfg, mode):
         _, b = ref.decode(rs, tb)
     assert max(errs) < E2E_TOL, errs
     hip.close()
+
+
+# ------------------------------------------- long contexts, attention splits
+# G = 7 query heads per kv head, as Qwen2.5-0.5B / 7B.
+LONG64 = O.QwenConfig(2048, 512, 2, 14, 2, 64, 1408, 1536, 1e-6, 1e6, False, 2047)
+LONG128 = O.QwenConfig(4096, 896, 2, 7, 1, 128, 2048, 1536, 1e-6, 1e6, True, 4095)
+LONG_PROMPT, LONG_STEPS = 1100, 6
+# (attn_split_tokens, attn_max_splits): the defaults (many splits merged
+# across workgroups), one split per kv head (a unit runs five 256-token
+# softmax chunks), three splits, and splits of at least 256 tokens.
+POLICIES = {"default": (0, 0), "one_split": (0, 1), "three_splits": (16, 3), "min256": (256, 32)}
+
+
+@pytest.fixture(scope="module", params=[LONG64, LONG128], ids=["hd64", "hd128"])
+def long_case(request):
+    """The oracle's teacher-forced trajectory: logits after a 1100-token
+    prompt and after each of 6 greedy tokens."""
+    cfg = request.param
+    src = O.OracleModel(cfg, 8)
+    from tests.model_pairs import fill_synthetic, oracle_for
+    fill_synthetic(src, 5)
+    ref = oracle_for(src, "int4")
+    prompt = list(O.synth_tokens(2, 0, LONG_PROMPT, cfg.vocab_size))
+    rs = ref.new_seq(cfg.max_context_tokens)
+    _, b = ref.prefill(rs, prompt)
+    traj, toks = [b], []
+    for _ in range(LONG_STEPS):
+        toks.append(O.argmax(b))
+        _, b = ref.decode(rs, toks[-1])
+        traj.append(b)
+    return cfg, prompt, toks, traj
+
+
+@pytest.mark.parametrize("policy", list(POLICIES), ids=list(POLICIES))
+def test_long_context_attention_splits(cuda, long_case, policy):
+    cfg, prompt, toks, traj = long_case
+    tok, ms = POLICIES[policy]
+    hip = M.HipModel.synthetic(cfg, seed=5, sigma=0.02,
+                               options=M.Options(quant="int4", attn_split_tokens=tok, attn_max_splits=ms))
+    s = hip.new_seq(cfg.max_context_tokens)
+    code, a = hip.prefill(s, prompt)
+    assert code == 0
+    for step in range(LONG_STEPS + 1):
+        err = rel_err(a, traj[step])
+        assert err < E2E_TOL, (step, err)
+        if step < LONG_STEPS:
+            assert O.argmax(a) == toks[step], f"step {step}, oracle top-2 gap {top2_gap(traj[step]):.3e}"
+            code, a = hip.decode(s, toks[step])
+            assert code == 0
+    hip.close()
+
+
+def test_long_context_split_policies_agree(cuda, long_case):
+    """Every split policy computes the same attention up to rounding: the
+    split changes the fp32 summation order, and fp16 rounding of the GEMV
+    inputs and cached K/V (2^-11 relative per flipped element) carries the
+    difference to the logits, so policies agree to well inside E2E_TOL but
+    not bit for bit."""
+    cfg, prompt, toks, traj = long_case
+    outs = []
+    for tok, ms in POLICIES.values():
+        hip = M.HipModel.synthetic(cfg, seed=5, sigma=0.02,
+                                   options=M.Options(quant="int4", attn_split_tokens=tok, attn_max_splits=ms))
+        s = hip.new_seq(cfg.max_context_tokens)
+        outs.append(hip.prefill(s, prompt)[1])
+        hip.close()
+    to_oracle = [rel_err(o, traj[0]) for o in outs]
+    between = [rel_err(o, outs[0]) for o in outs[1:]]
+    assert max(between) < 1.5e-3, (between, to_oracle)
+
+
+def test_batched_long_rows_match_sequential(cuda, long_case):
+    """Rows of different context lengths (different split counts) in one
+    batch: each row's logits equal its own sequential decode bit for bit."""
+    cfg, prompt, _, _ = long_case
+    hip = M.HipModel.synthetic(cfg, seed=5, sigma=0.02, options=M.Options(quant="int4"))
+    lens = [LONG_PROMPT, 37, 600, 260]
+    seq = [hip.new_seq(cfg.max_context_tokens) for _ in lens]
+    bat = [hip.new_seq(cfg.max_context_tokens) for _ in lens]
+    sl = [hip.prefill(s, prompt[:n])[1] for s, n in zip(seq, lens)]
+    bl = [hip.prefill(s, prompt[:n])[1] for s, n in zip(bat, lens)]
+    for step in range(3):
+        toks = [O.argmax(l) for l in sl]
+        for i in range(len(lens)):
+            assert np.array_equal(sl[i].view(np.uint32), bl[i].view(np.uint32)), (step, i)
+        sl = [hip.decode(s, t)[1] for s, t in zip(seq, toks)]
+        code, per, logits = hip.decode_batch(bat, toks)
+        assert code == 0 and per == [0] * len(lens)
+        bl = list(logits)
+    hip.close()
+
+
+@pytest.mark.parametrize("kw", [dict(attn_split_tokens=24), dict(attn_max_splits=33),
+                                dict(attn_split_tokens=-16), dict(kv_block_tokens=8)],
+                         ids=["tokens_not_tile_multiple", "too_many_splits", "negative", "block_not_16"])
+def test_attention_options_rejected(cuda, kw):
+    with pytest.raises(M.ModelError) as e:
+        M.HipModel.synthetic(MID, seed=1, options=M.Options(quant="int4", **kw))
+    assert e.value.code in (M.UNSUPPORTED_MODEL, M.INVALID_REQUEST)
