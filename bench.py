@@ -16,7 +16,15 @@ One JSON line is printed:
   cpu_baseline the reference engine's own CPU QwenModel (oracle/_ref), single
                thread as the reference runs it, on a bounded sample (see
                cpu_baseline.sample); the C restatement (oracle) if _ref is absent
+  roofline.traffic  HBM bytes per launch measured by rocprofv3 (FETCH_SIZE +
+               WRITE_SIZE, calibrated on a plain copy), read from
+               profiles/decode_step_traffic.json when that file was measured on
+               the same kernel and workload (bench_profile.py writes it); else null
 Only N=1 is supported: this build targets one GPU.
+
+  python bench.py --copy-calibration
+copies 1 GiB device to device 4 times (the runtime's plain copy kernel): the
+known-size reference that bench_profile.py scales the HBM counters by.
 """
 from __future__ import annotations
 
@@ -33,6 +41,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_step_traffic.json")
+COPY_BYTES = 1 << 30
 
 
 def log(*a):
@@ -90,6 +100,31 @@ def run_decode(args):
     hip.close()
     return dict(tok_s=args.steps / dt, ms=dt * 1e3 / args.steps, ctx_end=ctx, kernel_us=kernel_us,
                 step_bytes=step_bytes, gemv_bytes=gemv_bytes, tokens=toks)
+
+
+def copy_calibration():
+    """A plain device-to-device copy of COPY_BYTES, four times."""
+    import torch
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 4}), flush=True)
+
+
+def measured_traffic(kernel, workload):
+    """Bytes per launch from profiles/decode_step_traffic.json, if it was
+    measured on this kernel and workload."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel or t.get("workload") != workload:
+        return None
+    return t.get("traffic_bytes_per_launch")
 
 
 # ----------------------------------------------------------- CPU baseline
@@ -160,6 +195,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--quant", choices=["int4", "int8"], default="int4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -168,12 +204,17 @@ def main():
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    if args.copy_calibration:
+        copy_calibration()
+        return
     dec = run_decode(args)
     achieved = dec["step_bytes"] / (dec["kernel_us"] * 1e-6) / 1e9
     log(f"[bench] decode {dec['tok_s']:.1f} tok/s ({dec['ms']:.3f} ms/token wall, {dec['kernel_us']:.1f} us/step "
         f"on the stream, context {dec['ctx_end']}); {achieved:.0f} GB/s = {achieved / PEAK_HBM_GBS * 100:.1f}% of HBM peak")
+    kernel = f"decode_step_kernel<1, {args.quant}, 128> (fused decode step)"
+    workload = f"qwen2.5-7b {args.quant} bs1 prompt {args.prompt} greedy"
     roof = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None)
+                frac=round(achieved / PEAK_HBM_GBS, 4), traffic=measured_traffic(kernel, workload))
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
@@ -201,7 +242,7 @@ def main():
             "quant": args.quant,
         },
         "roofline": roof,
-        "roofline_kernel": {"kernel": f"decode_step_kernel<1, {args.quant}, 128> (fused decode step)",
+        "roofline_kernel": {"kernel": kernel, "workload": workload,
                             "avg_us": round(dec["kernel_us"], 2),
                             "bytes_per_launch": int(dec["step_bytes"])},
         "cpu_baseline": cpu,
