@@ -47,6 +47,7 @@ HipModelOptions ToOptions(const lyk_model_options* o) {
     opt.quantization = o->quant == 1 ? HipWeightQuant::kInt8 : HipWeightQuant::kInt4;
     opt.attn_split_tokens = o->attn_split_tokens;
     opt.attn_max_splits = o->attn_max_splits;
+    for (int i = 0; i < 5; ++i) opt.tile_rows[i] = o->tile_rows[i];
     return opt;
 }
 

@@ -61,6 +61,39 @@ inline int64_t src_row(int64_t t, int lane, int64_t n, int paired, int* which) {
 // Bit position of code j (0..7) within a 32-bit word of the q4 layout.
 constexpr int kNibblePos[8] = {0, 16, 4, 20, 8, 24, 12, 28};
 
+// Geometry of the tiled ("step") layouts: tiles of tr rows (paired: tr/2 rows
+// of each matrix), lane l of a block holding row l % tr and sub-block l / tr,
+// 4 blocks per chunk. unit = k values of one lane's block (32 q4, 16 q8).
+struct Tiled {
+    int64_t tiles, nb, nc;   // tiles; valid blocks and chunks per tile
+    int tr, lpr;
+};
+constexpr int kChunkBlocks = 4;
+
+bool tiled_of(int64_t n, int64_t k, int paired, int tr, int unit, Tiled* g) {
+    if (n <= 0 || k <= 0 || (tr != 16 && tr != 32 && tr != 64)) return false;
+    g->tr = tr;
+    g->lpr = 64 / tr;
+    g->tiles = paired ? (n + tr / 2 - 1) / (tr / 2) : (n + tr - 1) / tr;
+    const int64_t units = (k + unit - 1) / unit;
+    g->nb = (units + g->lpr - 1) / g->lpr;
+    g->nc = (g->nb + kChunkBlocks - 1) / kChunkBlocks;
+    return true;
+}
+
+// Source row of lane `lane` in tile t: (matrix 0/1, row) or -1 for padding.
+inline int64_t tiled_row(const Tiled& g, int64_t t, int lane, int64_t n, int paired, int* which) {
+    const int r = lane % g.tr;
+    if (paired) {
+        *which = r >= g.tr / 2;
+        const int64_t row = t * (g.tr / 2) + (r % (g.tr / 2));
+        return row < n ? row : -1;
+    }
+    *which = 0;
+    const int64_t row = t * g.tr + r;
+    return row < n ? row : -1;
+}
+
 }  // namespace
 }  // namespace lyk
 
@@ -200,6 +233,149 @@ int lyk_q8_pack(const int8_t* codes, const uint16_t* scales,
             }
         }
     });
+    return LYK_OK;
+}
+
+int lyk_q4_layout_tiled(int64_t n, int64_t k, int paired, int tile_rows,
+                        uint64_t* weight_bytes, uint64_t* scale_bytes) {
+    Tiled g;
+    if (!weight_bytes || !scale_bytes || !tiled_of(n, k, paired, tile_rows, 32, &g)) return LYK_ERR_INVALID_ARG;
+    *weight_bytes = uint64_t(g.tiles * g.nc * kChunkBlocks * 64 * 16);
+    *scale_bytes = uint64_t(g.tiles * g.nc * 64 * kChunkBlocks * 2);
+    return LYK_OK;
+}
+
+int lyk_q8_layout_tiled(int64_t n, int64_t k, int paired, int tile_rows,
+                        uint64_t* weight_bytes, uint64_t* scale_bytes) {
+    Tiled g;
+    if (!weight_bytes || !scale_bytes || !tiled_of(n, k, paired, tile_rows, 16, &g)) return LYK_ERR_INVALID_ARG;
+    *weight_bytes = uint64_t(g.tiles * g.nc * kChunkBlocks * 64 * 16);
+    *scale_bytes = uint64_t(g.tiles * 64 * 2);
+    return LYK_OK;
+}
+
+int lyk_q4_pack_tiled(const int8_t* codes, const uint16_t* scales,
+                      const int8_t* b_codes, const uint16_t* b_scales, int64_t n,
+                      int64_t k, int tile_rows, void* qw, void* qs) {
+    const int paired = b_codes != nullptr;
+    Tiled g;
+    if (!codes || !scales || !qw || !qs || !tiled_of(n, k, paired, tile_rows, 32, &g)) return LYK_ERR_INVALID_ARG;
+    if (paired && !b_scales) return LYK_ERR_INVALID_ARG;
+    const int64_t groups = (k + 31) / 32, NBp = g.nc * kChunkBlocks;
+    uint32_t* wout = static_cast<uint32_t*>(qw);
+    uint16_t* sout = static_cast<uint16_t*>(qs);
+    parallel_rows(g.tiles * 64, [&](int64_t i0, int64_t i1) {
+        for (int64_t i = i0; i < i1; ++i) {
+            const int64_t t = i / 64;
+            const int lane = int(i % 64), sub = lane / g.tr;
+            int which = 0;
+            const int64_t r = tiled_row(g, t, lane, n, paired, &which);
+            const int8_t* crow = r < 0 ? nullptr : (which ? b_codes : codes) + r * k;
+            const uint16_t* srow = r < 0 ? nullptr : (which ? b_scales : scales) + r * groups;
+            for (int64_t b = 0; b < NBp; ++b) {
+                const int64_t grp = b * g.lpr + sub;   // this lane's group in block b
+                uint32_t* dst = wout + ((t * NBp + b) * 64 + lane) * 4;
+                for (int d = 0; d < 4; ++d) {
+                    uint32_t word = 0;
+                    for (int j = 0; j < 8; ++j) {
+                        const int64_t kk = grp * 32 + d * 8 + j;
+                        const int q = (crow && kk < k) ? crow[kk] : 0;
+                        word |= uint32_t(q + 8) << kNibblePos[j];
+                    }
+                    dst[d] = word;
+                }
+                sout[((t * g.nc + b / kChunkBlocks) * 64 + lane) * kChunkBlocks + b % kChunkBlocks] =
+                    (srow && grp < groups) ? srow[grp] : uint16_t(0);
+            }
+        }
+    });
+    return LYK_OK;
+}
+
+int lyk_q8_pack_tiled(const int8_t* codes, const uint16_t* scales,
+                      const int8_t* b_codes, const uint16_t* b_scales, int64_t n,
+                      int64_t k, int tile_rows, void* qw, void* qs) {
+    const int paired = b_codes != nullptr;
+    Tiled g;
+    if (!codes || !scales || !qw || !qs || !tiled_of(n, k, paired, tile_rows, 16, &g)) return LYK_ERR_INVALID_ARG;
+    if (paired && !b_scales) return LYK_ERR_INVALID_ARG;
+    const int64_t NBp = g.nc * kChunkBlocks;
+    uint8_t* wout = static_cast<uint8_t*>(qw);
+    uint16_t* sout = static_cast<uint16_t*>(qs);
+    parallel_rows(g.tiles * 64, [&](int64_t i0, int64_t i1) {
+        for (int64_t i = i0; i < i1; ++i) {
+            const int64_t t = i / 64;
+            const int lane = int(i % 64), sub = lane / g.tr;
+            int which = 0;
+            const int64_t r = tiled_row(g, t, lane, n, paired, &which);
+            const int8_t* crow = r < 0 ? nullptr : (which ? b_codes : codes) + r * k;
+            for (int64_t b = 0; b < NBp; ++b) {
+                const int64_t kb = b * g.lpr + sub;   // this lane's 16-k block
+                uint8_t* dst = wout + ((t * NBp + b) * 64 + lane) * 16;
+                for (int j = 0; j < 16; ++j) {
+                    const int64_t kk = kb * 16 + j;
+                    const int q = (crow && kk < k) ? crow[kk] : 0;
+                    dst[j] = uint8_t(q + 128);
+                }
+            }
+            sout[t * 64 + lane] = r < 0 ? uint16_t(0) : (which ? b_scales : scales)[r];
+        }
+    });
+    return LYK_OK;
+}
+
+int lyk_q4_unpack_tiled(const void* qw, const void* qs, int64_t n, int64_t k, int paired,
+                        int tile_rows, int8_t* codes, uint16_t* scales) {
+    Tiled g;
+    if (!qw || !qs || !codes || !scales || !tiled_of(n, k, paired, tile_rows, 32, &g)) return LYK_ERR_INVALID_ARG;
+    const int64_t groups = (k + 31) / 32, NBp = g.nc * kChunkBlocks;
+    const uint32_t* win = static_cast<const uint32_t*>(qw);
+    const uint16_t* sin = static_cast<const uint16_t*>(qs);
+    for (int64_t t = 0; t < g.tiles; ++t)
+        for (int lane = 0; lane < 64; ++lane) {
+            int which = 0;
+            const int64_t r = tiled_row(g, t, lane, n, paired, &which);
+            if (r < 0) continue;
+            const int64_t row = r + (which ? n : 0), sub = lane / g.tr;
+            for (int64_t b = 0; b < NBp; ++b) {
+                const int64_t grp = b * g.lpr + sub;
+                if (grp >= groups) continue;
+                const uint32_t* src = win + ((t * NBp + b) * 64 + lane) * 4;
+                for (int d = 0; d < 4; ++d)
+                    for (int j = 0; j < 8; ++j) {
+                        const int64_t kk = grp * 32 + d * 8 + j;
+                        if (kk < k) codes[row * k + kk] = int8_t(int((src[d] >> kNibblePos[j]) & 15u) - 8);
+                    }
+                scales[row * groups + grp] = sin[((t * g.nc + b / kChunkBlocks) * 64 + lane) * kChunkBlocks + b % kChunkBlocks];
+            }
+        }
+    return LYK_OK;
+}
+
+int lyk_q8_unpack_tiled(const void* qw, const void* qs, int64_t n, int64_t k, int paired,
+                        int tile_rows, int8_t* codes, uint16_t* scales) {
+    Tiled g;
+    if (!qw || !qs || !codes || !scales || !tiled_of(n, k, paired, tile_rows, 16, &g)) return LYK_ERR_INVALID_ARG;
+    const int64_t NBp = g.nc * kChunkBlocks, kblocks = (k + 15) / 16;
+    const uint8_t* win = static_cast<const uint8_t*>(qw);
+    const uint16_t* sin = static_cast<const uint16_t*>(qs);
+    for (int64_t t = 0; t < g.tiles; ++t)
+        for (int lane = 0; lane < 64; ++lane) {
+            int which = 0;
+            const int64_t r = tiled_row(g, t, lane, n, paired, &which);
+            if (r < 0) continue;
+            const int64_t row = r + (which ? n : 0), sub = lane / g.tr;
+            for (int64_t b = 0; b < NBp; ++b) {
+                const int64_t kb = b * g.lpr + sub;
+                if (kb >= kblocks) continue;
+                const uint8_t* src = win + ((t * NBp + b) * 64 + lane) * 16;
+                for (int j = 0; j < 16; ++j) {
+                    const int64_t kk = kb * 16 + j;
+                    if (kk < k) codes[row * k + kk] = int8_t(int(src[j]) - 128);
+                }
+            }
+            scales[row] = sin[t * 64 + lane];
+        }
     return LYK_OK;
 }
 

@@ -123,6 +123,7 @@ struct PackedMat {
     DevBuf qw, qs;
     int64_t n = 0, k = 0;
     bool paired = false;
+    int tile_rows = 64;   // tiled layout height (lyk_q*_pack_tiled)
 };
 
 // FNV-1a 64, the prefix-cache chain hash (qwen_cuda_model.cu:1623-1630).
@@ -500,7 +501,7 @@ struct QwenHipModel::Impl {
 namespace {
 
 Status QuantizeUpload(bool q8, const std::vector<float>& a, const std::vector<float>* b, int64_t n,
-                      int64_t k, PackedMat& out, uint64_t& bytes) {
+                      int64_t k, int tile_rows, PackedMat& out, uint64_t& bytes) {
     const int64_t ns = q8 ? 1 : (k + 31) / 32;
     std::vector<int8_t> ca((size_t)(n * k)), cb;
     std::vector<uint16_t> sa((size_t)(n * ns)), sb;
@@ -514,14 +515,19 @@ Status QuantizeUpload(bool q8, const std::vector<float>& a, const std::vector<fl
                 : lyk_q4_quantize(b->data(), n, k, cb.data(), sb.data());
         if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight quantization failed", kComponent);
     }
+    // the tile height the fused step streams this shape best with on this device
+    const int tr = tile_rows ? tile_rows : lyk_hip_step_tile_rows(n, k, b != nullptr, q8 ? 1 : 0);
+    if (tr == 0) return Status(ErrorCode::kGpuUnhealthy, "hip device properties unavailable", kComponent);
+    if (tr != 16 && tr != 32 && tr != 64) return Status(ErrorCode::kUnsupportedModel, "tile height must be 16, 32 or 64", kComponent);
     uint64_t wb = 0, sbytes = 0;
-    rc = q8 ? lyk_q8_layout(n, k, b != nullptr, &wb, &sbytes) : lyk_q4_layout(n, k, b != nullptr, &wb, &sbytes);
+    rc = q8 ? lyk_q8_layout_tiled(n, k, b != nullptr, tr, &wb, &sbytes)
+            : lyk_q4_layout_tiled(n, k, b != nullptr, tr, &wb, &sbytes);
     if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight shape unsupported", kComponent);
     std::vector<uint8_t> qw(wb), qs(sbytes);
-    rc = q8 ? lyk_q8_pack(ca.data(), sa.data(), b ? cb.data() : nullptr, b ? sb.data() : nullptr, n, k,
-                          qw.data(), qs.data())
-            : lyk_q4_pack(ca.data(), sa.data(), b ? cb.data() : nullptr, b ? sb.data() : nullptr, n, k,
-                          qw.data(), qs.data());
+    rc = q8 ? lyk_q8_pack_tiled(ca.data(), sa.data(), b ? cb.data() : nullptr, b ? sb.data() : nullptr, n, k, tr,
+                                qw.data(), qs.data())
+            : lyk_q4_pack_tiled(ca.data(), sa.data(), b ? cb.data() : nullptr, b ? sb.data() : nullptr, n, k, tr,
+                                qw.data(), qs.data());
     if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight packing failed", kComponent);
     Status s = out.qw.Upload(qw.data(), qw.size());
     if (!s.ok()) return s;
@@ -530,7 +536,10 @@ Status QuantizeUpload(bool q8, const std::vector<float>& a, const std::vector<fl
     out.n = n;
     out.k = k;
     out.paired = b != nullptr;
-    bytes += wb + sbytes;
+    out.tile_rows = tr;
+    // bytes a step reads: codes and scales of the real rows (no tile padding)
+    const int64_t rows = n * (b ? 2 : 1);
+    bytes += q8 ? uint64_t(rows * k + rows * 2) : uint64_t(rows * ((k + 1) / 2) + rows * ((k + 31) / 32) * 2);
     return Status::Ok();
 }
 
@@ -619,23 +628,23 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
             LOAD_OR_RETURN(read(LayerName(l, nm), {std::string(nm).find("q_proj") != std::string::npos ? qd : kvd}, t));
             bias.insert(bias.end(), t.begin(), t.end());
         }
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, qkv, nullptr, int64_t(qd + 2 * kvd), int64_t(H), L.qkv, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, qkv, nullptr, int64_t(qd + 2 * kvd), int64_t(H), options.tile_rows[0], L.qkv, I.gemv_bytes));
         LOAD_OR_RETURN(UploadF32(bias, L.qkv_bias));
         LOAD_OR_RETURN(read(LayerName(l, "self_attn.o_proj.weight"), {H, qd}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(qd), L.o, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(qd), options.tile_rows[1], L.o, I.gemv_bytes));
         LOAD_OR_RETURN(read(LayerName(l, "mlp.gate_proj.weight"), {In, H}, a));
         LOAD_OR_RETURN(read(LayerName(l, "mlp.up_proj.weight"), {In, H}, b));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, &b, int64_t(In), int64_t(H), L.gateup, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, &b, int64_t(In), int64_t(H), options.tile_rows[2], L.gateup, I.gemv_bytes));
         LOAD_OR_RETURN(read(LayerName(l, "mlp.down_proj.weight"), {H, In}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(In), L.down, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(In), options.tile_rows[3], L.down, I.gemv_bytes));
     }
     LOAD_OR_RETURN(read("model.norm.weight", {H}, a));
     LOAD_OR_RETURN(UploadF32(a, I.final_norm));
     if (c.tie_word_embeddings) {
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, embed, nullptr, int64_t(V), int64_t(H), I.lm_head, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, embed, nullptr, int64_t(V), int64_t(H), options.tile_rows[4], I.lm_head, I.gemv_bytes));
     } else {
         LOAD_OR_RETURN(read("lm_head.weight", {V, H}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(V), int64_t(H), I.lm_head, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(V), int64_t(H), options.tile_rows[4], I.lm_head, I.gemv_bytes));
     }
     if (src.tensor_count() != expected) {
         r.status = Status(ErrorCode::kArtifactVerificationFailed, "weight file contains unexpected tensors",
@@ -702,6 +711,11 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
     md.num_blocks = int32_t(nblocks);
     md.attn_split_tokens = options.attn_split_tokens;
     md.attn_max_splits = options.attn_max_splits;
+    md.tile_rows[0] = I.layers[0].qkv.tile_rows;
+    md.tile_rows[1] = I.layers[0].o.tile_rows;
+    md.tile_rows[2] = I.layers[0].gateup.tile_rows;
+    md.tile_rows[3] = I.layers[0].down.tile_rows;
+    md.tile_rows[4] = I.lm_head.tile_rows;
     md.embed = I.embed.as<float>();
     md.final_norm = I.final_norm.as<float>();
     md.lm_head_w = I.lm_head.qw.p;

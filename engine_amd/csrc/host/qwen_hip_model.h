@@ -43,6 +43,9 @@ struct HipModelOptions {
     // multiple of 16; splits at most, <= 32); 0 = the kernel's defaults.
     int attn_split_tokens = 0;
     int attn_max_splits = 0;
+    // GEMV tile heights (16/32/64) for qkv, o, gate/up, down, LM head;
+    // 0 = the device's choice (lyk_hip_step_tile_rows).
+    int tile_rows[5] = {0, 0, 0, 0, 0};
 };
 
 // fp32 weights by reference tensor name. The safetensors file is one source;

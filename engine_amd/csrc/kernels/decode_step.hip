@@ -64,10 +64,15 @@ constexpr int kNormPer = 10;         // hidden_size <= kNormPer * kThreads
 constexpr int kMaxRows = 4;
 constexpr int kAttnMaxSplits = 32;   // context splits per (row, kv head), at most
 constexpr int kAttnSplitTokens = 32; // default: tokens per split, at least
+constexpr int kChunkBlocks = 4;      // 16-byte blocks per lane in a GEMV chunk
 constexpr int kMinPieceChunks = 4;   // K chunks per piece of a split tile, at least
 constexpr int kMaxPieces = 8;        // pieces per split tile, at most
 constexpr uint64_t kSpinTicks = 200000000ull;  // s_memrealtime is 100 MHz: 2 s
-constexpr size_t kMaxDynamicLds = 48 * 1024;
+constexpr size_t kMaxDynamicLds = 158 * 1024;   // of gfx950's 160 KiB per workgroup; the rest is static
+// Batches of up to kFoldRows rows fold the int4/int8 code offsets out of the
+// GEMV inner loop (a per-unit correction table beside the x window); wider
+// batches, whose windows leave no LDS for the table, subtract them in the loop.
+constexpr int kFoldRows = 2;
 
 struct StepArgs {
     lyk_step_model md;
@@ -178,30 +183,37 @@ __device__ __forceinline__ void block_sum_rows(float (&v)[M], int tid) {
 
 // ------------------------------------------------------------ GEMV phase
 
+// A matrix in the tiled layout (lyk_q*_pack_tiled): tiles of tr rows; lane l
+// of a block covers row l % tr and unit l / tr of the block's lpr = 64 / tr
+// units (a unit = 32 k for int4, 16 k for int8); 4 blocks per chunk.
 struct Mat {
     const u32x4* w;
     const void* s;
     int n;        // output rows (paired: rows of each matrix)
     int k;
+    int tr, lpr;  // rows per tile, lanes per row
     int tiles;
-    int chunks;   // K chunks of 8 groups (int4: 256 k) or 8 blocks (int8: 128 k)
+    int nb;       // valid blocks per tile
+    int chunks;   // chunks per tile
+    int ck;       // k values of one chunk
 };
 
 template <bool Q8>
-__device__ __forceinline__ Mat make_mat(const void* w, const void* s, int n, int k, bool paired) {
+__device__ __forceinline__ Mat make_mat(const void* w, const void* s, int n, int k, bool paired, int tr) {
     Mat m;
     m.w = static_cast<const u32x4*>(w);
     m.s = s;
     m.n = n;
     m.k = k;
-    m.tiles = paired ? (n + 31) / 32 : (n + 63) / 64;
+    m.tr = tr;
+    m.lpr = 64 / tr;
+    m.tiles = paired ? (n + tr / 2 - 1) / (tr / 2) : (n + tr - 1) / tr;
     const int unit = Q8 ? 16 : 32;
-    m.chunks = ((k + unit - 1) / unit + 7) / 8;
+    m.nb = ((k + unit - 1) / unit + m.lpr - 1) / m.lpr;
+    m.chunks = (m.nb + kChunkBlocks - 1) / kChunkBlocks;
+    m.ck = kChunkBlocks * m.lpr * unit;
     return m;
 }
-
-template <bool Q8>
-constexpr int chunk_k() { return Q8 ? 128 : 256; }
 
 // Pieces each row tile's K range is cut into: 1 unless the matrix has too
 // few tiles to give every workgroup work and each piece keeps at least
@@ -257,45 +269,71 @@ struct ChunkMath;
 
 template <int M>
 struct ChunkMath<M, false> {
-    static constexpr int CK = 256;
-    __device__ __forceinline__ static void load(const Mat& A, int f, int lane, u32x4 (&w)[8], u32x4& s4) {
-        const LYK_GLOBAL u32x4* wt = gp(A.w + (size_t)f * 512 + lane);
+    static constexpr int kUnit = 32;
+    // Chunk f (nv valid blocks): the lane's 4 blocks and its 4 group scales.
+    // Blocks past nv hold code 0 (nibble 8) without a load.
+    __device__ __forceinline__ static void load(const Mat& A, int f, int nv, int lane, u32x4 (&w)[kChunkBlocks],
+                                                u64& s) {
+        const LYK_GLOBAL u32x4* wt = gp(A.w + (size_t)f * (kChunkBlocks * 64) + lane);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            w[j] = __builtin_nontemporal_load(wt + j * 64);
+        for (int j = 0; j < kChunkBlocks; ++j) {
+            if (j < nv) w[j] = __builtin_nontemporal_load(wt + j * 64);
+            else w[j] = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
             __builtin_amdgcn_sched_barrier(0);
         }
-        s4 = __builtin_nontemporal_load(gp(static_cast<const u32x4*>(A.s) + (size_t)f * 64 + lane));
+        s = __builtin_nontemporal_load(gp(static_cast<const u64*>(A.s) + (size_t)f * 64 + lane));
         __builtin_amdgcn_sched_barrier(0);
     }
     // One group (32 codes) against x[32]: four independent dot2 chains.
-    __device__ __forceinline__ static float group(const u32x4& w, const u32x4* xv, uint32_t vmagic) {
-        const half2_t off_a = {(half_t)-1032.0f, (half_t)-1032.0f};
-        const half2_t off_b = {(half_t)-1152.0f, (half_t)-1152.0f};
+    // One group (32 codes) against x[32]. A code's low nibble reads as fp16
+    // 1024 + (q+8) and a high nibble as 1024 + 16(q+8) (one AND/OR each);
+    // their dot products with x carry the offsets, which the group's
+    // correction (1032 * sum of x at the low-nibble positions + 72 * sum at
+    // the high ones, computed once per x window) removes. Four independent
+    // dot2 chains.
+    // (Unfolded, for wide batches: the offsets come off each code first.)
+    __device__ __forceinline__ static float group(const u32x4& w, const u32x4* xv, uint32_t vmagic, float corr) {
+        constexpr bool fold = M <= kFoldRows;
+        const half2_t off_a = {(half_t)(fold ? 0.0f : -1032.0f), (half_t)(fold ? 0.0f : -1032.0f)};
+        const half2_t off_b = {(half_t)(fold ? 0.0f : -1152.0f), (half_t)(fold ? 0.0f : -1152.0f)};
         const uint32_t u4[4] = {w.x, w.y, w.z, w.w};
         float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const uint32_t u = u4[d], t = u >> 8;
             const u32x4 xx = xv[d];
-            a0 = dot2(as_half2((u & 0x000F000Fu) | vmagic) + off_a, as_half2(xx.x), a0);
-            b0 = dot2(as_half2((u & 0x00F000F0u) | vmagic) + off_b, as_half2(xx.y), b0);
-            a1 = dot2(as_half2((t & 0x000F000Fu) | vmagic) + off_a, as_half2(xx.z), a1);
-            b1 = dot2(as_half2((t & 0x00F000F0u) | vmagic) + off_b, as_half2(xx.w), b1);
+            half2_t ha = as_half2((u & 0x000F000Fu) | vmagic), hb = as_half2((u & 0x00F000F0u) | vmagic);
+            half2_t hc = as_half2((t & 0x000F000Fu) | vmagic), hd = as_half2((t & 0x00F000F0u) | vmagic);
+            if constexpr (!fold) {
+                ha += off_a;
+                hb += off_b;
+                hc += off_a;
+                hd += off_b;
+            }
+            a0 = dot2(ha, as_half2(xx.x), a0);
+            b0 = dot2(hb, as_half2(xx.y), b0);
+            a1 = dot2(hc, as_half2(xx.z), a1);
+            b1 = dot2(hd, as_half2(xx.w), b1);
         }
-        return (b0 + b1) * 0.0625f + (a0 + a1);
+        const float g = (b0 + b1) * 0.0625f + (a0 + a1);
+        if constexpr (fold) return g - corr;
+        return g;
     }
-    __device__ __forceinline__ static void compute(const u32x4 (&w)[8], const u32x4& s4, const uint16_t* xs,
-                                                   int xstride, float (&acc)[M], uint32_t vmagic) {
-        const uint32_t sw[4] = {s4.x, s4.y, s4.z, s4.w};
-        // groups in pairs: two groups' math interleaves, x of one pair at a time
+    // xc: the lane's x of block 0 of the chunk; block j is xstep halves on.
+    // cc: the lane's correction of block 0; block j is lpr entries on.
+    __device__ __forceinline__ static void compute(const u32x4 (&w)[kChunkBlocks], u64 s, const uint16_t* xc,
+                                                   const float* cc, int xstride, int cstride, int xstep, int lpr,
+                                                   float (&acc)[M], uint32_t vmagic) {
+        const uint32_t sw[2] = {(uint32_t)s, (uint32_t)(s >> 32)};
+        // blocks in pairs: two groups' math interleaves
 #pragma unroll
-        for (int j = 0; j < 8; j += 2) {
+        for (int j = 0; j < kChunkBlocks; j += 2) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const u32x4* x0 = reinterpret_cast<const u32x4*>(xs + (size_t)m * xstride + j * 32);
-                const float g0 = group(w[j], x0, vmagic);
-                const float g1 = group(w[j + 1], x0 + 4, vmagic);
+                const uint16_t* xm = xc + (size_t)m * xstride + j * xstep;
+                const float* cm = cc + (size_t)m * cstride + j * lpr;
+                const float g0 = group(w[j], reinterpret_cast<const u32x4*>(xm), vmagic, cm[0]);
+                const float g1 = group(w[j + 1], reinterpret_cast<const u32x4*>(xm + xstep), vmagic, cm[lpr]);
                 acc[m] = fmaf(g0, h2f(uint16_t(sw[j >> 1])), acc[m]);
                 acc[m] = fmaf(g1, h2f(uint16_t(sw[j >> 1] >> 16)), acc[m]);
             }
@@ -306,17 +344,25 @@ struct ChunkMath<M, false> {
 
 template <int M>
 struct ChunkMath<M, true> {
-    static constexpr int CK = 128;
-    __device__ __forceinline__ static void load(const Mat& A, int f, int lane, u32x4 (&w)[8], u32x4& s4) {
-        const LYK_GLOBAL u32x4* wt = gp(A.w + (size_t)f * 512 + lane);
+    static constexpr int kUnit = 16;
+    // Chunk f (nv valid blocks): the lane's 4 blocks; past nv, code 0 (128).
+    __device__ __forceinline__ static void load(const Mat& A, int f, int nv, int lane, u32x4 (&w)[kChunkBlocks],
+                                                u64& s) {
+        const LYK_GLOBAL u32x4* wt = gp(A.w + (size_t)f * (kChunkBlocks * 64) + lane);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            w[j] = __builtin_nontemporal_load(wt + j * 64);
+        for (int j = 0; j < kChunkBlocks; ++j) {
+            if (j < nv) w[j] = __builtin_nontemporal_load(wt + j * 64);
+            else w[j] = u32x4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
             __builtin_amdgcn_sched_barrier(0);
         }
-        (void)s4;
+        (void)s;
     }
-    __device__ __forceinline__ static float block(const u32x4& w, const u32x4* xv) {
+    // One block (16 codes) against x[16]: bytes q+128 read as fp16
+    // 1024 + (q+128) (one v_perm per pair); the block's correction
+    // (1152 * sum of its x) removes the offset.
+    // (Unfolded, for wide batches: the offset comes off each code first.)
+    __device__ __forceinline__ static float block(const u32x4& w, const u32x4* xv, float corr) {
+        constexpr bool fold = M <= kFoldRows;
         const half2_t off = {(half_t)-1152.0f, (half_t)-1152.0f};
         const uint32_t u4[4] = {w.x, w.y, w.z, w.w};
         const u32x4 x0 = xv[0], x1 = xv[1];
@@ -324,20 +370,29 @@ struct ChunkMath<M, true> {
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-            a0 = dot2(as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04010400u)) + off, as_half2(xw[2 * d]), a0);
-            a1 = dot2(as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04030402u)) + off, as_half2(xw[2 * d + 1]), a1);
+            half2_t lo = as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04010400u));
+            half2_t hi = as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04030402u));
+            if constexpr (!fold) {
+                lo += off;
+                hi += off;
+            }
+            a0 = dot2(lo, as_half2(xw[2 * d]), a0);
+            a1 = dot2(hi, as_half2(xw[2 * d + 1]), a1);
         }
+        if constexpr (fold) return (a0 + a1) - corr;
         return a0 + a1;
     }
-    __device__ __forceinline__ static void compute(const u32x4 (&w)[8], const u32x4&, const uint16_t* xs,
-                                                   int xstride, float (&acc)[M], uint32_t) {
+    __device__ __forceinline__ static void compute(const u32x4 (&w)[kChunkBlocks], u64, const uint16_t* xc,
+                                                   const float* cc, int xstride, int cstride, int xstep, int lpr,
+                                                   float (&acc)[M], uint32_t) {
 #pragma unroll
-        for (int j = 0; j < 8; j += 2) {
+        for (int j = 0; j < kChunkBlocks; j += 2) {
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const u32x4* x0 = reinterpret_cast<const u32x4*>(xs + (size_t)m * xstride + j * 16);
-                const float g0 = block(w[j], x0);
-                const float g1 = block(w[j + 1], x0 + 2);
+                const uint16_t* xm = xc + (size_t)m * xstride + j * xstep;
+                const float* cm = cc + (size_t)m * cstride + j * lpr;
+                const float g0 = block(w[j], reinterpret_cast<const u32x4*>(xm), cm[0]);
+                const float g1 = block(w[j + 1], reinterpret_cast<const u32x4*>(xm + xstep), cm[lpr]);
                 acc[m] += g0;
                 acc[m] += g1;
             }
@@ -392,7 +447,7 @@ __device__ __forceinline__ bool residual_add(const StepArgs& a, float (&h)[M][kN
 template <int M, bool Q8>
 __device__ __forceinline__ void norm_window(const StepArgs& a, const float (&h)[M][kNormPer], const float* gamma,
                                             const Mat& A, const Part& p, uint16_t* xs, int tid) {
-    constexpr int CK = chunk_k<Q8>();
+    const int CK = A.ck;
     const int H = a.md.hidden_size;
     float ss[M];
 #pragma unroll
@@ -427,42 +482,57 @@ __device__ __forceinline__ void norm_window(const StepArgs& a, const float (&h)[
     }
 }
 
-// x window <- fp16 of the tagged fp32 attention outputs [M][nq*hd] of the
-// window's chunks.
-template <int M, bool Q8>
-__device__ __forceinline__ bool fill_attn(const StepArgs& a, uint32_t tag, const Mat& A, const Part& p,
-                                          uint16_t* xs, int tid) {
-    constexpr int CK = chunk_k<Q8>();
-    if (!p.busy) return true;
-    const int kq = a.md.num_heads * a.md.head_dim;
-    const int total = M * p.win * CK;
+// Polls words src[0..n) (a word past `valid` reads as 0) into out(i, payload),
+// KB words per thread per round trip, so a window of up to 512*KB words costs
+// one memory round trip once its producers have written it.
+template <int KB, class Out>
+__device__ __forceinline__ bool poll_words(const StepArgs& a, const u64* src, int n, int valid, uint32_t tag,
+                                           int tid, Out out) {
     bool ok = true;
-    for (int e0 = tid; e0 < total; e0 += kThreads * 8) {
-        uint32_t v[8];
+    for (int e0 = tid; e0 < n; e0 += kThreads * KB) {
+        uint32_t v[KB];
         uint32_t have = 0;
         auto pending = [&]() {
             int missing = 0;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < KB; ++u) {
                 const int e = e0 + u * kThreads;
-                if (e >= total || (have >> u & 1)) continue;
-                const int m = e / (p.win * CK), k = p.ca * CK + e % (p.win * CK);
-                if (k >= kq) {
+                if (e >= n || (have >> u & 1)) continue;
+                if (e >= valid) {
                     v[u] = 0;
                     have |= 1u << u;
-                    continue;
+                } else if (take(src + e, tag, v[u])) {
+                    have |= 1u << u;
+                } else {
+                    ++missing;
                 }
-                if (take(a.attn_out + (size_t)m * kq + k, tag, v[u])) have |= 1u << u;
-                else ++missing;
             }
             return missing;
         };
         ok = spin(a, pending) && ok;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < KB; ++u) {
             const int e = e0 + u * kThreads;
-            if (e < total) xs[e] = f2h(bitsf(v[u]));
+            if (e < n) out(e, v[u]);
         }
+    }
+    return ok;
+}
+
+// x window <- fp16 of the tagged fp32 attention outputs [M][nq*hd] of the
+// window's chunks.
+template <int M, bool Q8>
+__device__ __forceinline__ bool fill_attn(const StepArgs& a, uint32_t tag, const Mat& A, const Part& p,
+                                          uint16_t* xs, int tid) {
+    if (!p.busy) return true;
+    const int CK = A.ck, kq = a.md.num_heads * a.md.head_dim;
+    const int n = p.win * CK, k0 = p.ca * CK;
+    bool ok = true;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        uint16_t* dst = xs + (size_t)m * n;
+        ok = poll_words<8>(a, a.attn_out + (size_t)m * kq + k0, n, kq - k0, tag, tid,
+                           [&](int e, uint32_t v) { dst[e] = f2h(bitsf(v)); }) && ok;
     }
     return ok;
 }
@@ -471,40 +541,16 @@ __device__ __forceinline__ bool fill_attn(const StepArgs& a, uint32_t tag, const
 template <int M, bool Q8>
 __device__ __forceinline__ bool fill_act(const StepArgs& a, uint32_t tag, const Mat& A, const Part& p,
                                          uint16_t* xs, int tid) {
-    constexpr int CK = chunk_k<Q8>();
-    constexpr int W = CK / 2;  // pairs per chunk row
     if (!p.busy) return true;
+    const int W = A.ck / 2;  // pairs per chunk
     const int In2 = a.md.intermediate_size / 2;
-    const int total = M * p.win * W;
-    uint32_t* dst = reinterpret_cast<uint32_t*>(xs);
+    const int n = p.win * W, i0 = p.ca * W;
     bool ok = true;
-    for (int e0 = tid; e0 < total; e0 += kThreads * 8) {
-        uint32_t v[8];
-        uint32_t have = 0;
-        auto pending = [&]() {
-            int missing = 0;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int e = e0 + u * kThreads;
-                if (e >= total || (have >> u & 1)) continue;
-                const int m = e / (p.win * W), r = e % (p.win * W);
-                const int pi = p.ca * W + r;   // pair index
-                if (pi >= In2) {
-                    v[u] = 0;
-                    have |= 1u << u;
-                    continue;
-                }
-                if (take(a.act + (size_t)m * In2 + pi, tag, v[u])) have |= 1u << u;
-                else ++missing;
-            }
-            return missing;
-        };
-        ok = spin(a, pending) && ok;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int e = e0 + u * kThreads;
-            if (e < total) dst[e] = v[u];
-        }
+    for (int m = 0; m < M; ++m) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(xs) + (size_t)m * n;
+        ok = poll_words<8>(a, a.act + (size_t)m * In2 + i0, n, In2 - i0, tag, tid,
+                            [&](int e, uint32_t v) { dst[e] = v; }) && ok;
     }
     return ok;
 }
@@ -531,7 +577,6 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                                           float (&h)[M][kNormPer], uint32_t tag0) {
     const int tid = phase_tid();
     using CM = ChunkMath<M, Q8>;
-    constexpr int CK = CM::CK;
     extern __shared__ __align__(16) unsigned char smem[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
     float* red = reinterpret_cast<float*>(smem);  // aliases xs after the stream
@@ -549,17 +594,29 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         case kDown: wp = Lw.down_w; sp = Lw.down_s; n = H; k = In; break;
         default: wp = a.md.lm_head_w; sp = a.md.lm_head_s; n = V; k = H; break;
     }
-    const Mat A = make_mat<Q8>(wp, sp, n, k, kind == kGateUp);
+    // matrices of a phase kind share a slot: qkv 0, o 1, gate/up 2, down 3, head 4
+    const int slot = kind == kQkv ? 0 : kind - 1;
+    const Mat A = make_mat<Q8>(wp, sp, n, k, kind == kGateUp, a.md.tile_rows[slot]);
+    const int CK = A.ck;
     mark(a, ph, 0);
     const Part p = partition(A);
     const int b = blockIdx.x;
     const int lane = tid & 63, wave = uniform(tid >> 6);
     const int len = p.f1 - p.f0;
     const int w0 = p.f0 + len * wave / kWaves, w1 = p.f0 + len * (wave + 1) / kWaves;
+    // valid blocks of chunk f: all but in a tile's last chunk when the tile's
+    // blocks do not fill it
+    const int tail = A.nb - (A.chunks - 1) * kChunkBlocks;
+    auto nv_of = [&](int f) { return tail == kChunkBlocks || (f + 1) % A.chunks ? kChunkBlocks : tail; };
 
-    u32x4 wa[8], wb[8], sa, sb;
-    if (w0 < w1) CM::load(A, w0, lane, wa, sa);
-    if (w0 + 1 < w1) CM::load(A, w0 + 1, lane, wb, sb);
+    // The wave's first two chunks are requested before the inputs are
+    // polled (streamed while waiting), the next two once they are in: the
+    // polls queue behind the loads issued before them, so the prefetch ahead
+    // of them is kept short.
+    u32x4 wa[kChunkBlocks], wb[kChunkBlocks], wc[kChunkBlocks], wd[kChunkBlocks];
+    u64 sa = 0, sb = 0, sc = 0, sd = 0;
+    if (w0 < w1) CM::load(A, w0, nv_of(w0), lane, wa, sa);
+    if (w0 + 1 < w1) CM::load(A, w0 + 1, nv_of(w0 + 1), lane, wb, sb);
 
     // ---- inputs
     bool ok = true;
@@ -590,6 +647,8 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     } else {
         ok = fill_act<M, Q8>(a, tag, A, p, xs, tid);
     }
+    if (w0 + 2 < w1) CM::load(A, w0 + 2, nv_of(w0 + 2), lane, wc, sc);
+    if (w0 + 3 < w1) CM::load(A, w0 + 3, nv_of(w0 + 3), lane, wd, sd);
     if (__syncthreads_or(!ok)) return false;
     mark(a, ph, 1);
     if (!p.busy) {
@@ -598,8 +657,37 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         return true;
     }
 
-    // ---- stream
+    // ---- offset corrections of the window's units (after the x window):
+    // int4 group 1032 * (x at k%8 in {0,1,4,5}) + 72 * (x at k%8 in {2,3,6,7});
+    // int8 block 1152 * sum of its 16 x
     const int xstride = p.win * CK;
+    const int cstride = xstride / CM::kUnit;
+    float* corr = reinterpret_cast<float*>(smem + ((size_t)M * xstride * 2 + 15) / 16 * 16);
+    for (int i = tid; i < (M <= kFoldRows ? M * cstride : 0); i += kThreads) {
+        const uint16_t* xu = xs + (size_t)i * CM::kUnit;   // rows are contiguous: unit i of the window
+        float c;
+        if constexpr (Q8) {
+            float s16 = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s16 += h2f(xu[e]);
+            c = 1152.0f * s16;
+        } else {
+            float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                if ((e & 2) == 0) sa += h2f(xu[e]);
+                else sb += h2f(xu[e]);
+            }
+            c = 1032.0f * sa + 72.0f * sb;
+        }
+        corr[i] = c;
+    }
+    if constexpr (M <= kFoldRows) __syncthreads();
+
+    // ---- stream
+    // this lane's unit within a block, and the distance between blocks, in x
+    const int usub = lane / A.tr;
+    const int xsub = usub * CM::kUnit, xstep = A.lpr * CM::kUnit;
     float accq[kPieces][M];
 #pragma unroll
     for (int q = 0; q < kPieces; ++q)
@@ -621,10 +709,12 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         float srow = 1.0f;
         if constexpr (Q8) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
         const int cend = p.pieces == 1 ? A.chunks : p.f1 - t * A.chunks;
-        // One chunk: math on the buffer, then request the chunk two ahead
+        // One chunk: math on the buffer, then request the chunk four ahead
         // into it; a tile's sums go to its piece slot when the tile ends.
-        auto step = [&](u32x4 (&wc)[8], u32x4& sc) -> bool {
-            CM::compute(wc, sc, xs + (size_t)(c - p.ca) * CK, xstride, acc, vmagic);
+        auto step = [&](u32x4 (&wbuf)[kChunkBlocks], u64& sbuf) -> bool {
+            CM::compute(wbuf, sbuf, xs + (size_t)(c - p.ca) * CK + xsub,
+                        corr + (size_t)(c - p.ca) * (CK / CM::kUnit) + usub, xstride, cstride, xstep, A.lpr, acc,
+                        vmagic);
             const bool end = f + 1 == w1;
             if (c + 1 == cend || c + 1 == A.chunks || end) {
 #pragma unroll
@@ -640,7 +730,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                     if (!end) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
             }
             if (end) return true;
-            if (f + 2 < w1) CM::load(A, f + 2, lane, wc, sc);
+            if (f + 4 < w1) CM::load(A, f + 4, nv_of(f + 4), lane, wbuf, sbuf);
             __builtin_amdgcn_sched_barrier(0);
             ++f;
             c = c + 1 == A.chunks ? 0 : c + 1;
@@ -649,10 +739,18 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         while (true) {
             if (step(wa, sa)) break;
             if (step(wb, sb)) break;
+            if (step(wc, sc)) break;
+            if (step(wd, sd)) break;
         }
     }
     __syncthreads();  // every wave is done with the x window
     mark(a, ph, 2);
+    // the lanes of one row (l, l+tr, ...) add their sums, in a fixed order
+#pragma unroll
+    for (int q = 0; q < kPieces; ++q)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            for (int o = A.tr; o < 64; o <<= 1) accq[q][m] += __shfl_xor(accq[q][m], o, 64);
     // each wave's tile sums, and the tiles [first, last] its range touched
     __shared__ int span[kWaves][2];
     {
@@ -726,32 +824,35 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
 #pragma unroll
                     for (int m = 0; m < M; ++m) v[m] += got[s2][m];
         }
-        const int r = t * 64 + lane;
+        // tile row `lane` (lanes below tr hold the rows' sums)
+        const int r = t * A.tr + lane;
+        const bool rv = lane < A.tr;
         switch (kind) {
             case kQkv:
-                if (r < rows)
+                if (rv && r < rows)
 #pragma unroll
                     for (int m = 0; m < M; ++m) put(a.qkv + (size_t)m * rows + r, fbits(v[m]), tag);
                 break;
             case kOut:
             case kDown: {
                 u64* dst = (kind == kOut ? a.d_attn : a.d_mlp) + (size_t)l * kMaxRows * H;
-                if (r < H)
+                if (rv && r < H)
 #pragma unroll
                     for (int m = 0; m < M; ++m) put(dst + (size_t)m * H + r, fbits(v[m]), tag);
                 break;
             }
             case kGateUp: {
-                // lanes 0-31 gate rows 32t.., lanes 32-63 the up rows; pairs
-                // of neighbouring rows go out as one word
-                const int j = t * 32 + lane;
+                // lanes 0..tr/2-1 hold gate rows t*tr/2.., lanes tr/2..tr-1
+                // the up rows; pairs of neighbouring rows go out as one word
+                const int half = A.tr / 2;
+                const int j = t * half + lane;
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    const float up = __shfl_down(v[m], 32, 64);
+                    const float up = __shfl_down(v[m], half, 64);
                     const float g = v[m];
                     const uint32_t act = f2h(g / (1.0f + expf(-g)) * up);
                     const uint32_t next = __shfl_down(act, 1, 64);
-                    if (lane < 32 && (lane & 1) == 0 && j < In)
+                    if (lane < half && (lane & 1) == 0 && j < In)
                         put(a.act + (size_t)m * (In / 2) + j / 2, act | (next << 16), tag);
                 }
                 break;
@@ -761,15 +862,16 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                 // index of the maximum, NaN never wins) and non-finite count
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    if (r < V) st(a.io.logits + (size_t)m * a.io.ld_logits + r, v[m]);
+                    const bool live = rv && r < V;
+                    if (live) st(a.io.logits + (size_t)m * a.io.ld_logits + r, v[m]);
                     if (!greedy) continue;
                     float x = v[m];
                     int bad = 0;
-                    if (r < V && !isfinite(x)) {
+                    if (live && !isfinite(x)) {
                         bad = 1;
                         if (isnan(x)) x = -INFINITY;
                     }
-                    Best bst = r < V ? Best{x, r} : Best{-INFINITY, 0x7fffffff};
+                    Best bst = live ? Best{x, r} : Best{-INFINITY, 0x7fffffff};
 #pragma unroll
                     for (int o = 32; o > 0; o >>= 1)
                         bst = better(bst, Best{__shfl_xor(bst.v, o, 64), __shfl_xor(bst.i, o, 64)});
@@ -1305,7 +1407,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
 
     if (a.io.mode == LYK_STEP_GREEDY && b == 0) {
         // ---- greedy token of row 0 (M == 1): first index of the maximum
-        const int V = a.md.vocab_size, tiles = (V + 63) / 64;
+        const int V = a.md.vocab_size, tiles = (V + a.md.tile_rows[4] - 1) / a.md.tile_rows[4];
         const uint32_t htag = tag0 | (uint32_t)L;
         mark(a, nph, 0);
         const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1366,11 +1468,49 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
 
 // ------------------------------------------------------------ host side
 
-int chunks_of(int64_t k, bool q8) {
-    const int unit = q8 ? 16 : 32;
-    return (int)(((k + unit - 1) / unit + 7) / 8);
+// Tiles and chunks of an [n, k] matrix in the tiled layout of tile height tr.
+void tiled_shape(int64_t n, int64_t k, bool paired, bool q8, int tr, int64_t& tiles, int64_t& chunks,
+                 int64_t& ck) {
+    const int lpr = 64 / tr, unit = q8 ? 16 : 32;
+    tiles = paired ? (n + tr / 2 - 1) / (tr / 2) : (n + tr - 1) / tr;
+    const int64_t nb = ((k + unit - 1) / unit + lpr - 1) / lpr;
+    chunks = (nb + kChunkBlocks - 1) / kChunkBlocks;
+    ck = (int64_t)kChunkBlocks * lpr * unit;
 }
 
+// Tile height for an [n, k] matrix on a grid of `grid` workgroups: the
+// tallest whose busiest workgroup streams at most 15% more chunks than the
+// average busy one (tiles split into K pieces where there are few, each piece
+// polling only its share of the input window); failing that, the one whose
+// busiest workgroup streams least. Taller tiles also keep a wave's lanes on
+// more rows, so fewer lane sums to combine.
+int choose_tile_rows(int64_t n, int64_t k, bool paired, bool q8, int grid) {
+    int best = 0;
+    int64_t best_max = -1;
+    for (int tr : {64, 32, 16}) {
+        int64_t tiles, chunks, ck;
+        tiled_shape(n, k, paired, q8, tr, tiles, chunks, ck);
+        const int pieces = tile_pieces((int)tiles, (int)chunks, grid);
+        int64_t per_wg, busy;
+        if (pieces == 1) {
+            busy = tiles < grid ? tiles : grid;
+            per_wg = (tiles + busy - 1) / busy * chunks;
+        } else {
+            busy = tiles * pieces;
+            per_wg = (chunks + pieces - 1) / pieces;
+        }
+        // a wave's chunk range may touch at most kPieces tiles
+        const int64_t lw = (per_wg + kWaves - 1) / kWaves;
+        if (1 + (lw - 1 + chunks - 1) / chunks > kPieces) continue;
+        const double avg = (double)tiles * chunks / (double)busy;
+        if ((double)per_wg <= 1.15 * avg) return tr;
+        if (best_max < 0 || per_wg < best_max) {
+            best = tr;
+            best_max = per_wg;
+        }
+    }
+    return best ? best : 64;
+}
 
 // Head dims with a compiled attention path.
 bool head_dim_supported(int hd) { return hd == 4 || hd == 64 || hd == 128; }
@@ -1404,33 +1544,35 @@ int check_model(const lyk_step_model& md) {
         return LYK_ERR_INVALID_ARG;
     if (md.hidden_size > kNormPer * kThreads || (md.intermediate_size & 1) || md.num_layers > 255)
         return LYK_ERR_SHAPE;
+    for (int i = 0; i < 5; ++i)
+        if (md.tile_rows[i] != 16 && md.tile_rows[i] != 32 && md.tile_rows[i] != 64) return LYK_ERR_INVALID_ARG;
     return LYK_OK;
 }
 
-// The five GEMVs of a step: {rows, k, paired}.
+// The five GEMVs of a step: {rows, k, paired, tile height}.
 struct MatShape {
     int64_t n, k;
     bool paired;
+    int tr;
 };
 void step_mats(const lyk_step_model& md, MatShape (&out)[5]) {
     const int64_t H = md.hidden_size, In = md.intermediate_size, nq = md.num_heads, nkv = md.num_kv_heads,
                   hd = md.head_dim;
-    out[0] = {(nq + 2 * nkv) * hd, H, false};
-    out[1] = {H, nq * hd, false};
-    out[2] = {In, H, true};
-    out[3] = {H, In, false};
-    out[4] = {md.vocab_size, H, false};
+    out[0] = {(nq + 2 * nkv) * hd, H, false, md.tile_rows[0]};
+    out[1] = {H, nq * hd, false, md.tile_rows[1]};
+    out[2] = {In, H, true, md.tile_rows[2]};
+    out[3] = {H, In, false, md.tile_rows[3]};
+    out[4] = {md.vocab_size, H, false, md.tile_rows[4]};
 }
 
 struct PhaseShape {
-    int64_t tiles, chunks, range, win;  // range: chunks of one workgroup, at most
+    int64_t tiles, chunks, range, win, ck;  // range: chunks of one workgroup, at most
     int pieces;
 };
 PhaseShape phase_shape(const MatShape& mt, bool q8, int grid) {
     PhaseShape ps;
-    ps.tiles = mt.paired ? (mt.n + 31) / 32 : (mt.n + 63) / 64;
-    ps.chunks = chunks_of(mt.k, q8);
-    ps.pieces = tile_pieces(ps.tiles, ps.chunks, grid);
+    tiled_shape(mt.n, mt.k, mt.paired, q8, mt.tr, ps.tiles, ps.chunks, ps.ck);
+    ps.pieces = tile_pieces((int)ps.tiles, (int)ps.chunks, grid);
     if (ps.pieces == 1) {
         const int64_t gp = ps.tiles < grid ? ps.tiles : grid;
         ps.range = (ps.tiles + gp - 1) / gp * ps.chunks;
@@ -1460,7 +1602,7 @@ Layout layout(const lyk_step_model& md, int rows, int grid) {
         if (ps.pieces > 1) dpart_words = std::max<uint64_t>(dpart_words, (uint64_t)ps.tiles * ps.pieces * rows * 64);
     }
     L.dpart_stride = (dpart_words * 8 + 255) / 256 * 256 / 8;
-    const int64_t head_tiles = (md.vocab_size + 63) / 64;
+    const int64_t head_tiles = (md.vocab_size + md.tile_rows[4] - 1) / md.tile_rows[4];
     uint64_t at = 0;
     auto take = [&](uint64_t bytes) {
         const uint64_t o = at;
@@ -1487,13 +1629,14 @@ Layout layout(const lyk_step_model& md, int rows, int grid) {
 // GEMV phase, or the attention buffers.
 size_t lds_bytes(const lyk_step_model& md, int rows, int grid) {
     const bool q8 = md.q8 != 0;
-    const int ck = q8 ? 128 : 256;
     MatShape mats[5];
     step_mats(md, mats);
     size_t need = (size_t)kWaves * kPieces * rows * 64 * 4;
     for (const MatShape& mt : mats) {
         const PhaseShape ps = phase_shape(mt, q8, grid);
-        need = std::max(need, (size_t)rows * ps.win * ck * 2);
+        const size_t unit = q8 ? 16 : 32;
+        const size_t corr = rows <= kFoldRows ? (size_t)rows * ps.win * ps.ck / unit * 4 : 0;
+        need = std::max(need, ((size_t)rows * ps.win * ps.ck * 2 + 15) / 16 * 16 + corr);
     }
     // attention: q high/low parts, chunk weights high/low, current k and v
     // (fp16), current k (fp32), then the larger of the chunk scores, the raw
@@ -1522,9 +1665,20 @@ bool pieces_ok(const lyk_step_model& md, int grid) {
 template <int M, bool Q8, int HD>
 int launch(const StepArgs* d_args, int grid, size_t lds, hipStream_t st) {
     auto kern = decode_step_kernel<M, Q8, HD>;
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kThreads, lds) != hipSuccess || occ < 1)
-        return LYK_ERR_SHAPE;
+    // Dynamic LDS beyond the default limit needs the kernel's opt-in; done
+    // once per instantiation (the attribute holds for the process).
+    static const bool opted_in =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kMaxDynamicLds) == hipSuccess;
+    if (!opted_in) return LYK_ERR_LAUNCH;
+    // one workgroup per CU must fit (registers, LDS); checked once per LDS size
+    static thread_local size_t fits_lds = 0;
+    if (fits_lds != lds) {
+        int occ = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kThreads, lds) != hipSuccess || occ < 1)
+            return LYK_ERR_SHAPE;
+        fits_lds = lds;
+    }
     void* params[] = {&d_args};
     if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(grid), dim3(kThreads), params,
                                    (unsigned)lds, st) != hipSuccess)
@@ -1574,7 +1728,8 @@ uint64_t lyk_hip_step_workspace_bytes(const lyk_step_model* model, int max_rows)
     if (!model || max_rows < 1 || max_rows > kMaxRows || check_model(*model) != LYK_OK) return 0;
     const int grid = step_grid();
     if (!pieces_ok(*model, grid)) return 0;
-    if (lds_bytes(*model, max_rows, grid) > kMaxDynamicLds) return 0;
+    for (int m = 1; m <= max_rows; ++m)   // narrow batches carry the fold's correction table
+        if (lds_bytes(*model, m, grid) > kMaxDynamicLds) return 0;
     return layout(*model, max_rows, grid).total;
 }
 
@@ -1586,6 +1741,12 @@ uint32_t lyk_hip_step_phases(const lyk_step_model* model, int mode) {
 }
 
 int lyk_hip_step_grid(void) { return step_grid(); }
+
+int lyk_hip_step_tile_rows(int64_t n, int64_t k, int paired, int q8) {
+    const int grid = step_grid();
+    if (n <= 0 || k <= 0 || grid < 1) return 0;
+    return choose_tile_rows(n, k, paired != 0, q8 != 0, grid);
+}
 
 int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void* d_workspace,
                         uint64_t workspace_bytes, int max_rows, void* stream) {

@@ -42,6 +42,12 @@ _KERNEL_SIGS = {
     "lyk_q8_quantize": (I, [P, I64, I64, P, P]),
     "lyk_q4_pack": (I, [P, P, P, P, I64, I64, P, P]),
     "lyk_q8_pack": (I, [P, P, P, P, I64, I64, P, P]),
+    "lyk_q4_layout_tiled": (I, [I64, I64, I, I, C.POINTER(U64), C.POINTER(U64)]),
+    "lyk_q8_layout_tiled": (I, [I64, I64, I, I, C.POINTER(U64), C.POINTER(U64)]),
+    "lyk_q4_pack_tiled": (I, [P, P, P, P, I64, I64, I, P, P]),
+    "lyk_q8_pack_tiled": (I, [P, P, P, P, I64, I64, I, P, P]),
+    "lyk_q4_unpack_tiled": (I, [P, P, I64, I64, I, I, P, P]),
+    "lyk_q8_unpack_tiled": (I, [P, P, I64, I64, I, I, P, P]),
     "lyk_hip_q4_unpack": (I, [P, P, I64, I64, I, P, P, P]),
     "lyk_hip_q8_unpack": (I, [P, P, I64, I64, I, P, P, P]),
     "lyk_hip_q4_dequant": (I, [P, P, I64, I64, I, P, P]),
@@ -60,6 +66,7 @@ _KERNEL_SIGS = {
     "lyk_hip_step_workspace_bytes": (U64, [P, I]),
     "lyk_hip_step_phases": (U32, [P, I]),
     "lyk_hip_step_grid": (I, []),
+    "lyk_hip_step_tile_rows": (I, [I64, I64, I, I]),
     "lyk_hip_decode_step": (I, [P, P, P, U64, I, P]),
     "lyk_hip_step_reset": (I, [P, U64, P]),
     "lyk_hip_step_error": (I, [P, C.POINTER(C.c_int32), P]),
@@ -76,7 +83,8 @@ class ModelConfig(C.Structure):
 class ModelOptions(C.Structure):
     _fields_ = [("device_id", C.c_int32), ("kv_pool_tokens", C.c_uint32),
                 ("kv_block_tokens", C.c_uint32), ("quant", C.c_int32),
-                ("attn_split_tokens", C.c_int32), ("attn_max_splits", C.c_int32)]
+                ("attn_split_tokens", C.c_int32), ("attn_max_splits", C.c_int32),
+                ("tile_rows", C.c_int32 * 5)]
 
 
 I32P = C.POINTER(C.c_int32)

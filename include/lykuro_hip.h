@@ -94,6 +94,39 @@ int lyk_q8_pack(const int8_t* codes, const uint16_t* scales,
                 const int8_t* b_codes, const uint16_t* b_scales, int64_t n,
                 int64_t k, void* qw, void* qs);
 
+/* Tiled layouts of the fused decode step (lyk_hip_decode_step). Same codes,
+ * nibble order and scales as above, cut for a chosen tile height tr in
+ * {16, 32, 64} so that a matrix of few rows still spreads over every CU
+ * without splitting rows across workgroups.
+ *   Tile t holds tr rows (paired: rows 0..tr/2-1 from A, tr/2..tr-1 from B,
+ *   matrix rows t*tr/2..). Lane l of a block covers tile row l % tr and
+ *   sub-block s = l / tr of the block's 64/tr: block b of the tile gives lane
+ *   l the 16 bytes of unit u = b*(64/tr) + s of that row, a unit being one
+ *   32-code group (q4, same word order as above) or 16 codes (q8, bytes
+ *   q+128). Blocks go 4 to a chunk; NB = ceil(units / (64/tr)) valid blocks
+ *   per tile, NC = ceil(NB/4) chunks, NBp = 4*NC.
+ *   q4 codes: qw[((t*NBp + b)*64 + l)*16], scales fp16
+ *     qs[((t*NC + c)*64 + l)*4 + j] = scale of the lane's unit in block 4c+j.
+ *   q8 codes: qw[((t*NBp + b)*64 + l)*16], scales qs[t*64 + l] = the fp16 row
+ *     scale of the lane's row.
+ * Padding (rows past n, units past k) is code 0 with scale 0. */
+int lyk_q4_layout_tiled(int64_t n, int64_t k, int paired, int tile_rows,
+                        uint64_t* weight_bytes, uint64_t* scale_bytes);
+int lyk_q8_layout_tiled(int64_t n, int64_t k, int paired, int tile_rows,
+                        uint64_t* weight_bytes, uint64_t* scale_bytes);
+int lyk_q4_pack_tiled(const int8_t* codes, const uint16_t* scales,
+                      const int8_t* b_codes, const uint16_t* b_scales, int64_t n,
+                      int64_t k, int tile_rows, void* qw, void* qs);
+int lyk_q8_pack_tiled(const int8_t* codes, const uint16_t* scales,
+                      const int8_t* b_codes, const uint16_t* b_scales, int64_t n,
+                      int64_t k, int tile_rows, void* qw, void* qs);
+/* Host-side inverse of the tiled packing (tests): row-major codes and scales
+ * (paired: the 2n rows A then B). */
+int lyk_q4_unpack_tiled(const void* qw, const void* qs, int64_t n, int64_t k,
+                        int paired, int tile_rows, int8_t* codes, uint16_t* scales);
+int lyk_q8_unpack_tiled(const void* qw, const void* qs, int64_t n, int64_t k,
+                        int paired, int tile_rows, int8_t* codes, uint16_t* scales);
+
 /* Device-side inverse of the packing (for tests and diagnostics): writes the
  * row-major codes and scales of the matrix (paired: the 2n rows A then B). */
 int lyk_hip_q4_unpack(const void* d_qw, const void* d_qs, int64_t n,
@@ -249,6 +282,10 @@ typedef struct lyk_step_model {
      * whole 16-token tiles, at least attn_split_tokens (a multiple of 16) long,
      * at most attn_max_splits (<= 32) of them; 0 selects the defaults (32, 32). */
     int32_t attn_split_tokens, attn_max_splits;
+    /* Tile height (16, 32 or 64) each GEMV matrix was packed with
+     * (lyk_q*_pack_tiled), in the order qkv, o, gate/up, down, LM head;
+     * lyk_hip_step_tile_rows gives the one this device runs best. */
+    int32_t tile_rows[5];
     const float* embed;      /* fp32 [vocab][hidden] */
     const float* final_norm;
     const void* lm_head_w;
@@ -293,6 +330,10 @@ uint64_t lyk_hip_step_workspace_bytes(const lyk_step_model* model, int max_rows)
  * the trace holds lyk_hip_step_grid() * (4*phases + 2) values. */
 uint32_t lyk_hip_step_phases(const lyk_step_model* model, int mode);
 int lyk_hip_step_grid(void);
+/* Tile height to pack an [n, k] GEMV matrix with for the step on this device
+ * (paired: gate/up; q8: int8 weights): the one whose busiest workgroup
+ * streams the least; 0 on invalid arguments. */
+int lyk_hip_step_tile_rows(int64_t n, int64_t k, int paired, int q8);
 /* Launches one step (stream-ordered, asynchronous). Positions must be
  * < rope_positions and have their blocks in the tables; the host checks
  * both. The launch arguments are kept in the workspace and uploaded only when

@@ -41,6 +41,9 @@ typedef struct lyk_model_options {
     /* attention context split (lyk_step_model fields of the same names);
      * 0 selects the defaults */
     int32_t attn_split_tokens, attn_max_splits;
+    /* GEMV tile heights (16/32/64) for qkv, o, gate/up, down, LM head;
+     * 0 = lyk_hip_step_tile_rows' choice for this device */
+    int32_t tile_rows[5];
 } lyk_model_options;
 
 /* QwenHipModel::Load from a safetensors file (replaces QwenCudaModel::Load,

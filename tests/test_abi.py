@@ -156,3 +156,59 @@ def test_invalid_arguments_rejected():
                                None, 0, None, 0, None) == 1
     assert lib.lyk_hip_gemv_q4(1, 1, 64, 64, 8, 64, 5, 0, 8, 64, None, 0, None, 0, None) == 1
     assert lib.lyk_hip_gemv_q4(1, 1, 64, 64, 8, 48, 1, 0, 8, 64, None, 0, None, 0, None) == 1
+
+
+@pytest.mark.parametrize("mode", ["int4", "int8"])
+@pytest.mark.parametrize("tr", [16, 32, 64])
+@pytest.mark.parametrize("n,k,paired", [(1, 16, False), (70, 100, False), (45, 300, True), (96, 512, False),
+                                        (33, 4160, True)])
+def test_tiled_pack_round_trip(mode, tr, n, k, paired):
+    """The fused step's tiled layouts: pack then unpack returns the codes and
+    scales exactly, for every tile height, ragged n and k, paired or not."""
+    lib = L.kernels()
+    rng = np.random.default_rng(n * 7 + k + tr)
+    q8 = mode == "int8"
+    ns = 1 if q8 else (k + 31) // 32
+    mats = []
+    for _ in range(2 if paired else 1):
+        w = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+        codes = np.zeros((n, k), np.int8)
+        scales = np.zeros((n, ns), np.uint16)
+        quant = lib.lyk_q8_quantize if q8 else lib.lyk_q4_quantize
+        assert quant(w.ctypes.data, n, k, codes.ctypes.data, scales.ctypes.data) == 0
+        mats.append((codes, scales))
+    wb, sb = C.c_uint64(), C.c_uint64()
+    layout = lib.lyk_q8_layout_tiled if q8 else lib.lyk_q4_layout_tiled
+    assert layout(n, k, int(paired), tr, C.byref(wb), C.byref(sb)) == 0
+    qw = np.full(wb.value, 0xAB, np.uint8)
+    qs = np.full(sb.value, 0xCD, np.uint8)
+    pack = lib.lyk_q8_pack_tiled if q8 else lib.lyk_q4_pack_tiled
+    b = mats[1] if paired else (None, None)
+    assert pack(mats[0][0].ctypes.data, mats[0][1].ctypes.data,
+                b[0].ctypes.data if paired else None, b[1].ctypes.data if paired else None,
+                n, k, tr, qw.ctypes.data, qs.ctypes.data) == 0
+    rows = 2 * n if paired else n
+    out_c = np.zeros((rows, k), np.int8)
+    out_s = np.zeros((rows, ns), np.uint16)
+    unpack = lib.lyk_q8_unpack_tiled if q8 else lib.lyk_q4_unpack_tiled
+    assert unpack(qw.ctypes.data, qs.ctypes.data, n, k, int(paired), tr,
+                  out_c.ctypes.data, out_s.ctypes.data) == 0
+    want_c = np.concatenate([m[0] for m in mats])
+    want_s = np.concatenate([m[1] for m in mats])
+    assert np.array_equal(out_c, want_c)
+    assert np.array_equal(out_s, want_s)
+    # every byte of both buffers is written: packing over another fill
+    # pattern gives the same bytes
+    qw2 = np.full(wb.value, 0x12, np.uint8)
+    qs2 = np.full(sb.value, 0x34, np.uint8)
+    assert pack(mats[0][0].ctypes.data, mats[0][1].ctypes.data,
+                b[0].ctypes.data if paired else None, b[1].ctypes.data if paired else None,
+                n, k, tr, qw2.ctypes.data, qs2.ctypes.data) == 0
+    assert np.array_equal(qw, qw2) and np.array_equal(qs, qs2)
+
+
+def test_tiled_layout_rejects_bad_tile_rows():
+    lib = L.kernels()
+    wb, sb = C.c_uint64(), C.c_uint64()
+    for tr in (0, 8, 48, 128):
+        assert lib.lyk_q4_layout_tiled(64, 64, 0, tr, C.byref(wb), C.byref(sb)) == 1

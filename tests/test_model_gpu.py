@@ -95,12 +95,21 @@ def test_rejects_capacity_overrun_and_bad_tokens(tiny):
     assert hip.decode(hip.new_seq(8), 303)[0] == M.INVALID_REQUEST
 
 
-def test_batched_decode_matches_sequential(tiny):
-    """cuda_parity_test.cpp:206-256, with a stronger bar: the GEMV and
-    attention arithmetic of a row does not depend on the batch, so batched
-    logits equal sequential ones bit for bit."""
+# Batches of up to two rows fold the quantization offsets out of the GEMV
+# loop exactly as single rows do, so their rows' logits equal sequential
+# decoding bit for bit; wider batches subtract the offsets per code and agree
+# to rounding (BATCH_TOL), with equal greedy tokens as the reference requires.
+BATCH_TOL = 1e-3
+
+
+@pytest.mark.parametrize("prompts", [[[1, 5, 9], [17, 4, 22, 8, 30]],
+                                     [[1, 5, 9], [17, 4, 22, 8, 30], [7, 7, 25], [300, 2]]],
+                         ids=["rows2_bit_exact", "rows4"])
+def test_batched_decode_matches_sequential(tiny, prompts):
+    """cuda_parity_test.cpp:206-256 (greedy tokens equal), and for batches
+    of two the stronger bar: logits equal bit for bit."""
     mode, _, _, hip = tiny
-    prompts = [[1, 5, 9], [17, 4, 22, 8, 30], [7, 7, 25], [300, 2]]
+    exact = len(prompts) <= 2
     seq = [hip.new_seq(64) for _ in prompts]
     bat = [hip.new_seq(64) for _ in prompts]
     sl = [hip.prefill(s, p)[1] for s, p in zip(seq, prompts)]
@@ -109,11 +118,16 @@ def test_batched_decode_matches_sequential(tiny):
         toks = [O.argmax(l) for l in sl]
         assert toks == [O.argmax(l) for l in bl]
         for i in range(len(prompts)):
-            assert np.array_equal(sl[i].view(np.uint32), bl[i].view(np.uint32)), (step, i)
+            if exact:
+                assert np.array_equal(sl[i].view(np.uint32), bl[i].view(np.uint32)), (step, i)
+            else:
+                assert rel_err(bl[i], sl[i]) < BATCH_TOL, (step, i)
         sl = [hip.decode(s, t)[1] for s, t in zip(seq, toks)]
         code, per, logits = hip.decode_batch(bat, toks)
         assert code == 0 and per == [0] * len(prompts)
         bl = list(logits)
+    for x in seq + bat:
+        x.close()
 
 
 def test_batched_decode_isolates_invalid_items(tiny):
@@ -327,20 +341,26 @@ def test_long_context_split_policies_agree(cuda, long_case):
     assert max(between) < 1.5e-3, (between, to_oracle)
 
 
-def test_batched_long_rows_match_sequential(cuda, long_case):
+@pytest.mark.parametrize("lens", [[LONG_PROMPT, 37], [LONG_PROMPT, 37, 600, 260]], ids=["rows2", "rows4"])
+def test_batched_long_rows_match_sequential(cuda, long_case, lens):
     """Rows of different context lengths (different split counts) in one
-    batch: each row's logits equal its own sequential decode bit for bit."""
+    batch: each row's logits equal its own sequential decode (bit for bit
+    for batches of two, to BATCH_TOL for four)."""
     cfg, prompt, _, _ = long_case
     hip = M.HipModel.synthetic(cfg, seed=5, sigma=0.02, options=M.Options(quant="int4"))
-    lens = [LONG_PROMPT, 37, 600, 260]
+    exact = len(lens) <= 2
     seq = [hip.new_seq(cfg.max_context_tokens) for _ in lens]
     bat = [hip.new_seq(cfg.max_context_tokens) for _ in lens]
     sl = [hip.prefill(s, prompt[:n])[1] for s, n in zip(seq, lens)]
     bl = [hip.prefill(s, prompt[:n])[1] for s, n in zip(bat, lens)]
     for step in range(3):
         toks = [O.argmax(l) for l in sl]
+        assert toks == [O.argmax(l) for l in bl]
         for i in range(len(lens)):
-            assert np.array_equal(sl[i].view(np.uint32), bl[i].view(np.uint32)), (step, i)
+            if exact:
+                assert np.array_equal(sl[i].view(np.uint32), bl[i].view(np.uint32)), (step, i)
+            else:
+                assert rel_err(bl[i], sl[i]) < BATCH_TOL, (step, i)
         sl = [hip.decode(s, t)[1] for s, t in zip(seq, toks)]
         code, per, logits = hip.decode_batch(bat, toks)
         assert code == 0 and per == [0] * len(lens)
