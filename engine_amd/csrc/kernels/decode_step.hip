@@ -1338,23 +1338,26 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
             }
         }
         if (__syncthreads_or(!ok)) return false;
-        if (tid < G) {
-            float mx = -INFINITY;
-            for (int sp = 0; sp < Sm; ++sp) mx = fmaxf(mx, mlv[(sp * G + tid) * 2]);
-            float L = 0.0f;
-            for (int sp = 0; sp < Sm; ++sp) {
-                const float es = expf(mlv[(sp * G + tid) * 2] - mx);
-                mlv[(sp * G + tid) * 2] = es;
-                L += mlv[(sp * G + tid) * 2 + 1] * es;
-            }
-            lsum[tid] = L;
+        // split weights e_s = exp(m_s - max) and the total sum, one wave per
+        // head and a lane per split (splits <= 32 < 64)
+        for (int h = wave; h < G; h += kWaves) {
+            const bool live = lane < Sm;
+            const float ms = live ? mlv[(lane * G + h) * 2] : -INFINITY;
+            const float mx = wave_max(ms);
+            const float es = live ? expf(ms - mx) : 0.0f;
+            const float L = wave_sum(live ? mlv[(lane * G + h) * 2 + 1] * es : 0.0f);
+            if (live) mlv[(lane * G + h) * 2] = es;
+            if (lane == 0) lsum[h] = L;
         }
         __syncthreads();
         u64* out = a.attn_out + (size_t)m * kq + (size_t)g * GH;
         for (int k = tid; k < ne; k += kThreads) {
             const int h = (e0 + k) / HD;
-            float o = 0.0f;
-            for (int sp = 0; sp < Sm; ++sp) o += vals[k * Sm + sp] * mlv[(sp * G + h) * 2];
+            // four interleaved partial sums (independent LDS loads), added in
+            // a fixed order
+            float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int sp = 0; sp < Sm; ++sp) o4[sp & 3] += vals[k * Sm + sp] * mlv[(sp * G + h) * 2];
+            const float o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
             put(&out[e0 + k], fbits(o / lsum[h]), tag);
         }
         __syncthreads();   // LDS is rewritten by the next unit
