@@ -48,6 +48,7 @@ HipModelOptions ToOptions(const lyk_model_options* o) {
     opt.attn_split_tokens = o->attn_split_tokens;
     opt.attn_max_splits = o->attn_max_splits;
     for (int i = 0; i < 5; ++i) opt.tile_rows[i] = o->tile_rows[i];
+    opt.lds_prefetch = o->lds_prefetch;
     return opt;
 }
 

@@ -711,6 +711,7 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
     md.num_blocks = int32_t(nblocks);
     md.attn_split_tokens = options.attn_split_tokens;
     md.attn_max_splits = options.attn_max_splits;
+    md.lds_prefetch = options.lds_prefetch;
     md.tile_rows[0] = I.layers[0].qkv.tile_rows;
     md.tile_rows[1] = I.layers[0].o.tile_rows;
     md.tile_rows[2] = I.layers[0].gateup.tile_rows;

@@ -46,6 +46,9 @@ struct HipModelOptions {
     // GEMV tile heights (16/32/64) for qkv, o, gate/up, down, LM head;
     // 0 = the device's choice (lyk_hip_step_tile_rows).
     int tile_rows[5] = {0, 0, 0, 0, 0};
+    // Gate/up chunks per wave staged in LDS ahead of the gate/up phase:
+    // 0 = as many as fit, -1 = none, n > 0 = at most n.
+    int lds_prefetch = 0;
 };
 
 // fp32 weights by reference tensor name. The safetensors file is one source;

@@ -56,6 +56,8 @@ __device__ __forceinline__ float wave_max(float v) {
 // the LDS wait counter and so serialize LDS reads behind outstanding global
 // loads.
 #define LYK_GLOBAL __attribute__((address_space(1)))
+// LDS address space (the destination operand of LDS DMA).
+#define LYK_LOCAL __attribute__((address_space(3)))
 template <class T>
 __device__ __forceinline__ LYK_GLOBAL T* gp(T* p) {
     return (LYK_GLOBAL T*)p;

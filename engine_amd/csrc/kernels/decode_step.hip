@@ -30,7 +30,8 @@
 //     lane), its 8 waves split the tile's K chunks and combine in LDS. When a
 //     matrix has too few tiles for the grid (down projection) every tile's K
 //     range is cut into pieces; piece 0's workgroup adds the others' tagged
-//     partials in piece order. The activation vector sits in LDS.
+//     partials in piece order (for QKV, attention adds the pieces as it
+//     reads them). The activation vector sits in LDS.
 //   * Attention units are (row, kv head, context split), q.k and p.v on the
 //     matrix cores; the splits of a kv head merge in split order, each split
 //     finishing a slice of the outputs.
@@ -92,6 +93,8 @@ struct StepArgs {
     int attn_split_tokens;  // context tokens per attention split, at least (multiple of 16)
     int attn_max_splits;    // attention splits per (row, kv head), at most
     int phases;             // phases of one launch (trace layout)
+    int pf_off;             // LDS byte offset of the gate/up staging region
+    int pf_chunks;          // gate/up chunks per wave staged there (0: none)
 };
 
 // ------------------------------------------------------------ primitives
@@ -284,6 +287,15 @@ struct ChunkMath<M, false> {
         s = __builtin_nontemporal_load(gp(static_cast<const u64*>(A.s) + (size_t)f * 64 + lane));
         __builtin_amdgcn_sched_barrier(0);
     }
+    // The same from a chunk staged in LDS (stage_chunk's layout).
+    __device__ __forceinline__ static void load_lds(const unsigned char* slot, int nv, int lane,
+                                                    u32x4 (&w)[kChunkBlocks], u64& s) {
+#pragma unroll
+        for (int j = 0; j < kChunkBlocks; ++j)
+            w[j] = j < nv ? reinterpret_cast<const u32x4*>(slot + j * 1024)[lane]
+                          : u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+        s = reinterpret_cast<const u64*>(slot + kChunkBlocks * 1024)[lane];
+    }
     // One group (32 codes) against x[32]: four independent dot2 chains.
     // One group (32 codes) against x[32]. A code's low nibble reads as fp16
     // 1024 + (q+8) and a high nibble as 1024 + 16(q+8) (one AND/OR each);
@@ -357,6 +369,14 @@ struct ChunkMath<M, true> {
         }
         (void)s;
     }
+    __device__ __forceinline__ static void load_lds(const unsigned char* slot, int nv, int lane,
+                                                    u32x4 (&w)[kChunkBlocks], u64& s) {
+#pragma unroll
+        for (int j = 0; j < kChunkBlocks; ++j)
+            w[j] = j < nv ? reinterpret_cast<const u32x4*>(slot + j * 1024)[lane]
+                          : u32x4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+        (void)s;
+    }
     // One block (16 codes) against x[16]: bytes q+128 read as fp16
     // 1024 + (q+128) (one v_perm per pair); the block's correction
     // (1152 * sum of its x) removes the offset.
@@ -401,6 +421,52 @@ struct ChunkMath<M, true> {
     }
 };
 
+// ------------------------------------------------------------ gate/up staging
+
+// LDS bytes of one staged chunk: its blocks lane-major (64 lanes x 16 B
+// each), then for int4 the lanes' group scales (64 x 8 B).
+template <bool Q8>
+constexpr int kSlotBytes = kChunkBlocks * 1024 + (Q8 ? 0 : 512);
+
+// Requests into LDS the first pf_chunks chunks of every wave's share of the
+// layer's gate/up matrix (gemv_step's split: the workgroup's range cut evenly
+// over its waves), by LDS DMA: no registers are held, and completion counts
+// in the issuing wave's vmcnt, so each wave stages the chunks it will itself
+// consume. Called once the workgroup's attention work is done: the loads
+// stream while the attention and O phases wait on their inputs, which have
+// little HBM traffic of their own.
+template <bool Q8>
+__device__ __forceinline__ void stage_gateup(const StepArgs& a, const lyk_step_layer& Lw) {
+    if (a.pf_chunks == 0) return;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const Mat A = make_mat<Q8>(Lw.gateup_w, Lw.gateup_s, a.md.intermediate_size, a.md.hidden_size, true,
+                               a.md.tile_rows[2]);
+    const Part p = partition(A);
+    if (!p.busy) return;
+    const int tid = phase_tid();
+    const int lane = tid & 63, wave = uniform(tid >> 6);
+    const int len = p.f1 - p.f0;
+    const int w0 = p.f0 + len * wave / kWaves, w1 = p.f0 + len * (wave + 1) / kWaves;
+    const int n = min(a.pf_chunks, w1 - w0);
+    const int tail = A.nb - (A.chunks - 1) * kChunkBlocks;
+    unsigned char* base = smem + a.pf_off + wave * a.pf_chunks * kSlotBytes<Q8>;
+    for (int i = 0; i < n; ++i) {
+        const int f = w0 + i;
+        const int nv = tail == kChunkBlocks || (f + 1) % A.chunks ? kChunkBlocks : tail;
+        unsigned char* slot = base + i * kSlotBytes<Q8>;
+        for (int j = 0; j < nv; ++j)
+            __builtin_amdgcn_global_load_lds(gp(A.w + ((size_t)f * kChunkBlocks + j) * 64 + lane),
+                                             (LYK_LOCAL void*)(slot + j * 1024), 16, 0, 0);
+        if constexpr (!Q8) {
+            if (lane < 32) {
+                const u32x4* sv = reinterpret_cast<const u32x4*>(static_cast<const u64*>(A.s) + (size_t)f * 64);
+                __builtin_amdgcn_global_load_lds(gp(sv + lane), (LYK_LOCAL void*)(slot + kChunkBlocks * 1024), 16,
+                                                 0, 0);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------ phase inputs
 
 // Residual rows (registers, element i = tid + j*kThreads of each row) plus
@@ -442,11 +508,26 @@ __device__ __forceinline__ bool residual_add(const StepArgs& a, float (&h)[M][kN
     return true;
 }
 
+// The gamma values of this thread's residual elements that fall in the
+// workgroup's window, requested before the residual poll so that their
+// latency overlaps the wait.
+__device__ __forceinline__ void load_gamma(const StepArgs& a, const float* gamma, const Mat& A, const Part& p,
+                                           int tid, float (&g)[kNormPer]) {
+    const int H = a.md.hidden_size;
+#pragma unroll
+    for (int j = 0; j < kNormPer; ++j) {
+        const int i = tid + j * kThreads;
+        const int slot = i / A.ck - p.ca;
+        g[j] = p.busy && i < H && slot >= 0 && slot < p.win ? ld(gamma + i) : 0.0f;
+    }
+}
+
 // x window <- fp16 RMSNorm(h) * gamma over the chunks of the window, zero
 // beyond k (the reference order: h * (1/sqrt(mean(h^2) + eps)) * gamma).
 template <int M, bool Q8>
-__device__ __forceinline__ void norm_window(const StepArgs& a, const float (&h)[M][kNormPer], const float* gamma,
-                                            const Mat& A, const Part& p, uint16_t* xs, int tid) {
+__device__ __forceinline__ void norm_window(const StepArgs& a, const float (&h)[M][kNormPer],
+                                            const float (&gv)[kNormPer], const Mat& A, const Part& p,
+                                            uint16_t* xs, int tid) {
     const int CK = A.ck;
     const int H = a.md.hidden_size;
     float ss[M];
@@ -467,7 +548,7 @@ __device__ __forceinline__ void norm_window(const StepArgs& a, const float (&h)[
         if (i < H) {
             const int slot = i / CK - p.ca;
             if (slot >= 0 && slot < p.win) {
-                const float g = ld(gamma + i);
+                const float g = gv[j];
 #pragma unroll
                 for (int m = 0; m < M; ++m)
                     xs[((size_t)m * p.win + slot) * CK + (i % CK)] = f2h(h[m][j] * scale[m] * g);
@@ -608,15 +689,21 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     // blocks do not fill it
     const int tail = A.nb - (A.chunks - 1) * kChunkBlocks;
     auto nv_of = [&](int f) { return tail == kChunkBlocks || (f + 1) % A.chunks ? kChunkBlocks : tail; };
+    // gate/up: the wave's chunks [w0, w0 + npf) wait in LDS (stage_gateup);
+    // the register pipeline starts after them
+    const int npf = kind == kGateUp ? min(a.pf_chunks, w1 - w0) : 0;
+    const int g0 = w0 + npf;
+    const unsigned char* pfb = smem + a.pf_off + wave * a.pf_chunks * kSlotBytes<Q8>;
+    if (npf > 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // The wave's first two chunks are requested before the inputs are
-    // polled (streamed while waiting), the next two once they are in: the
-    // polls queue behind the loads issued before them, so the prefetch ahead
-    // of them is kept short.
+    // The wave's first two register chunks are requested before the inputs
+    // are polled (streamed while waiting), the next two once they are in:
+    // the polls queue behind the loads issued before them, so the prefetch
+    // ahead of them is kept short.
     u32x4 wa[kChunkBlocks], wb[kChunkBlocks], wc[kChunkBlocks], wd[kChunkBlocks];
     u64 sa = 0, sb = 0, sc = 0, sd = 0;
-    if (w0 < w1) CM::load(A, w0, nv_of(w0), lane, wa, sa);
-    if (w0 + 1 < w1) CM::load(A, w0 + 1, nv_of(w0 + 1), lane, wb, sb);
+    if (g0 < w1) CM::load(A, g0, nv_of(g0), lane, wa, sa);
+    if (g0 + 1 < w1) CM::load(A, g0 + 1, nv_of(g0 + 1), lane, wb, sb);
 
     // ---- inputs
     bool ok = true;
@@ -640,15 +727,17 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
             dtag = tag - 1;
             gamma = a.md.final_norm;
         }
+        float gv[kNormPer];
+        load_gamma(a, gamma, A, p, tid, gv);
         if (d) ok = residual_add<M>(a, h, d, dtag, tid);
-        if (ok && p.busy) norm_window<M, Q8>(a, h, gamma, A, p, xs, tid);
+        if (ok && p.busy) norm_window<M, Q8>(a, h, gv, A, p, xs, tid);
     } else if (kind == kOut) {
         ok = fill_attn<M, Q8>(a, tag, A, p, xs, tid);
     } else {
         ok = fill_act<M, Q8>(a, tag, A, p, xs, tid);
     }
-    if (w0 + 2 < w1) CM::load(A, w0 + 2, nv_of(w0 + 2), lane, wc, sc);
-    if (w0 + 3 < w1) CM::load(A, w0 + 3, nv_of(w0 + 3), lane, wd, sd);
+    if (g0 + 2 < w1) CM::load(A, g0 + 2, nv_of(g0 + 2), lane, wc, sc);
+    if (g0 + 3 < w1) CM::load(A, g0 + 3, nv_of(g0 + 3), lane, wd, sd);
     if (__syncthreads_or(!ok)) return false;
     mark(a, ph, 1);
     if (!p.busy) {
@@ -709,9 +798,10 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         float srow = 1.0f;
         if constexpr (Q8) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
         const int cend = p.pieces == 1 ? A.chunks : p.f1 - t * A.chunks;
-        // One chunk: math on the buffer, then request the chunk four ahead
-        // into it; a tile's sums go to its piece slot when the tile ends.
-        auto step = [&](u32x4 (&wbuf)[kChunkBlocks], u64& sbuf) -> bool {
+        // One chunk: math on the buffer, then (register chunks) request the
+        // chunk four ahead into it; a tile's sums go to its piece slot when
+        // the tile ends.
+        auto step = [&](u32x4 (&wbuf)[kChunkBlocks], u64& sbuf, bool refill) -> bool {
             CM::compute(wbuf, sbuf, xs + (size_t)(c - p.ca) * CK + xsub,
                         corr + (size_t)(c - p.ca) * (CK / CM::kUnit) + usub, xstride, cstride, xstep, A.lpr, acc,
                         vmagic);
@@ -730,17 +820,24 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                     if (!end) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
             }
             if (end) return true;
-            if (f + 4 < w1) CM::load(A, f + 4, nv_of(f + 4), lane, wbuf, sbuf);
+            if (refill && f + 4 < w1) CM::load(A, f + 4, nv_of(f + 4), lane, wbuf, sbuf);
             __builtin_amdgcn_sched_barrier(0);
             ++f;
             c = c + 1 == A.chunks ? 0 : c + 1;
             return false;
         };
-        while (true) {
-            if (step(wa, sa)) break;
-            if (step(wb, sb)) break;
-            if (step(wc, sc)) break;
-            if (step(wd, sd)) break;
+        bool done = false;
+        for (int i = 0; i < npf && !done; ++i) {
+            u32x4 wl[kChunkBlocks];
+            u64 sl = 0;
+            CM::load_lds(pfb + i * kSlotBytes<Q8>, nv_of(f), lane, wl, sl);
+            done = step(wl, sl, false);
+        }
+        while (!done) {
+            if (step(wa, sa, true)) break;
+            if (step(wb, sb, true)) break;
+            if (step(wc, sc, true)) break;
+            if (step(wd, sd, true)) break;
         }
     }
     __syncthreads();  // every wave is done with the x window
@@ -1009,8 +1106,13 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         g = r / Sm;
         s = r % Sm;
     };
+    // units go to the workgroups from the top of the grid down: the QKV
+    // tiles fill the grid from the bottom, so the first units land on
+    // workgroups with no QKV work, which reach this phase early and have
+    // their K/V loads in flight when q arrives
+    const int rb = (int)gridDim.x - 1 - (int)blockIdx.x;
     bool ok = true;
-    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+    for (int u = rb; u < units; u += gridDim.x) {
         int m, g, s, Sm, Tm, ctx;
         unit_of(u, m, g, s, Sm, Tm, ctx);
         const int pos = ctx - 1;
@@ -1165,7 +1267,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 store_sc1_u16(Lw.v_cache + base + (size_t)i * bt + pos % bt, vcur[i]);
             }
         }
-        if (u == (int)blockIdx.x) mark(a, ph, 1);
+        if (u == rb) mark(a, ph, 1);
 
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};   // O[4*quad + j][dv]
         const int nch = (t1 - t0 + kChunkT - 1) / kChunkT;
@@ -1276,7 +1378,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
             }
             __syncthreads();   // scores and weights are rewritten by the next chunk
         }
-        if (u == (int)blockIdx.x) mark(a, ph, 2);
+        if (u == rb) mark(a, ph, 2);
         const size_t grp = (size_t)m * nkv + g;
         if (wave < DB && dv < HD) {
             u64* out = a.attn_out + (size_t)m * kq + (size_t)g * GH;
@@ -1300,7 +1402,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
 
     // merge: unit s of a split kv head finishes outputs [s*E, (s+1)*E) of
     // its G*HD: out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max)
-    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+    for (int u = rb; u < units; u += gridDim.x) {
         int m, g, s, Sm, Tm, ctx;
         unit_of(u, m, g, s, Sm, Tm, ctx);
         if (Sm == 1) continue;
@@ -1406,6 +1508,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
         const bool ok = kind == kAttn ? attention_phase<M, HD>(a, ph, Lw, tag0 | (uint32_t)l)
                                       : gemv_step<M, Q8>(a, ph, kind, l, Lw, h, tag0);
         if (!ok) return;
+        if (kind == kAttn) stage_gateup<Q8>(a, Lw);
     }
 
     if (a.io.mode == LYK_STEP_GREEDY && b == 0) {
@@ -1549,6 +1652,7 @@ int check_model(const lyk_step_model& md) {
         return LYK_ERR_SHAPE;
     for (int i = 0; i < 5; ++i)
         if (md.tile_rows[i] != 16 && md.tile_rows[i] != 32 && md.tile_rows[i] != 64) return LYK_ERR_INVALID_ARG;
+    if (md.lds_prefetch < -1) return LYK_ERR_INVALID_ARG;
     return LYK_OK;
 }
 
@@ -1630,17 +1734,46 @@ Layout layout(const lyk_step_model& md, int rows, int grid) {
 
 // Dynamic LDS of a launch: the largest x window or reduction buffer of any
 // GEMV phase, or the attention buffers.
+// LDS of a GEMV phase: its x window (+ the fold's correction table), or the
+// reduction buffer it aliases after the stream.
+size_t gemv_lds(const MatShape& mt, bool q8, int rows, int grid) {
+    const PhaseShape ps = phase_shape(mt, q8, grid);
+    const size_t unit = q8 ? 16 : 32;
+    const size_t corr = rows <= kFoldRows ? (size_t)rows * ps.win * ps.ck / unit * 4 : 0;
+    return std::max((size_t)kWaves * kPieces * rows * 64 * 4,
+                    ((size_t)rows * ps.win * ps.ck * 2 + 15) / 16 * 16 + corr);
+}
+
+// The gate/up staging region (stage_gateup): above the LDS of the O and
+// gate/up phases, which run while it is held, as many chunks per wave as
+// fit (and the option allows), at most a wave's share.
+struct Staging {
+    int off, chunks;
+    size_t end;
+};
+Staging gateup_staging(const lyk_step_model& md, int rows, int grid) {
+    const bool q8 = md.q8 != 0;
+    MatShape mats[5];
+    step_mats(md, mats);
+    Staging sg;
+    sg.off = (int)((std::max(gemv_lds(mats[1], q8, rows, grid), gemv_lds(mats[2], q8, rows, grid)) + 255) / 256 * 256);
+    const int64_t slot = q8 ? 4096 : 4608;
+    const PhaseShape ps = phase_shape(mats[2], q8, grid);
+    int64_t chunks = ((int64_t)kMaxDynamicLds - sg.off) / (kWaves * slot);
+    chunks = std::min<int64_t>(chunks, (ps.range + kWaves - 1) / kWaves);
+    if (md.lds_prefetch < 0) chunks = 0;
+    else if (md.lds_prefetch > 0) chunks = std::min<int64_t>(chunks, md.lds_prefetch);
+    sg.chunks = (int)std::max<int64_t>(chunks, 0);
+    sg.end = sg.chunks ? (size_t)sg.off + (size_t)sg.chunks * kWaves * slot : 0;
+    return sg;
+}
+
 size_t lds_bytes(const lyk_step_model& md, int rows, int grid) {
     const bool q8 = md.q8 != 0;
     MatShape mats[5];
     step_mats(md, mats);
-    size_t need = (size_t)kWaves * kPieces * rows * 64 * 4;
-    for (const MatShape& mt : mats) {
-        const PhaseShape ps = phase_shape(mt, q8, grid);
-        const size_t unit = q8 ? 16 : 32;
-        const size_t corr = rows <= kFoldRows ? (size_t)rows * ps.win * ps.ck / unit * 4 : 0;
-        need = std::max(need, ((size_t)rows * ps.win * ps.ck * 2 + 15) / 16 * 16 + corr);
-    }
+    size_t need = gateup_staging(md, rows, grid).end;
+    for (const MatShape& mt : mats) need = std::max(need, gemv_lds(mt, q8, rows, grid));
     // attention: q high/low parts, chunk weights high/low, current k and v
     // (fp16), current k (fp32), then the larger of the chunk scores, the raw
     // q and the merge's (max, sum) table + partial slice
@@ -1791,6 +1924,9 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     a.attn_split_tokens = model->attn_split_tokens ? model->attn_split_tokens : kAttnSplitTokens;
     a.attn_max_splits = model->attn_max_splits ? model->attn_max_splits : kAttnMaxSplits;
     a.phases = (int)lyk_hip_step_phases(model, io->mode);
+    const Staging sg = gateup_staging(*model, m, grid);
+    a.pf_off = sg.off;
+    a.pf_chunks = sg.chunks;
     hipStream_t st = static_cast<hipStream_t>(stream);
     StepArgs* d_args = reinterpret_cast<StepArgs*>(ws + L.args);
     {

@@ -84,7 +84,7 @@ class ModelOptions(C.Structure):
     _fields_ = [("device_id", C.c_int32), ("kv_pool_tokens", C.c_uint32),
                 ("kv_block_tokens", C.c_uint32), ("quant", C.c_int32),
                 ("attn_split_tokens", C.c_int32), ("attn_max_splits", C.c_int32),
-                ("tile_rows", C.c_int32 * 5)]
+                ("tile_rows", C.c_int32 * 5), ("lds_prefetch", C.c_int32)]
 
 
 I32P = C.POINTER(C.c_int32)

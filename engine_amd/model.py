@@ -67,11 +67,12 @@ class Options:
     attn_split_tokens: int = 0   # 0: the kernel's defaults
     attn_max_splits: int = 0
     tile_rows: tuple = (0, 0, 0, 0, 0)   # qkv, o, gate/up, down, head; 0: device choice
+    lds_prefetch: int = 0   # gate/up chunks per wave staged in LDS: 0 as many as fit, -1 none
 
     def c(self):
         return L.ModelOptions(self.device_id, self.kv_pool_tokens, self.kv_block_tokens,
                               1 if self.quant == "int8" else 0, self.attn_split_tokens,
-                              self.attn_max_splits, (C.c_int32 * 5)(*self.tile_rows))
+                              self.attn_max_splits, (C.c_int32 * 5)(*self.tile_rows), self.lds_prefetch)
 
 
 class HipModel:

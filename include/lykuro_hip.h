@@ -286,6 +286,9 @@ typedef struct lyk_step_model {
      * (lyk_q*_pack_tiled), in the order qkv, o, gate/up, down, LM head;
      * lyk_hip_step_tile_rows gives the one this device runs best. */
     int32_t tile_rows[5];
+    /* Gate/up chunks per wave staged in LDS while the attention and O phases
+     * run: 0 = as many as fit, -1 = none, n > 0 = at most n. */
+    int32_t lds_prefetch;
     const float* embed;      /* fp32 [vocab][hidden] */
     const float* final_norm;
     const void* lm_head_w;

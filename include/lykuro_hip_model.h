@@ -44,6 +44,8 @@ typedef struct lyk_model_options {
     /* GEMV tile heights (16/32/64) for qkv, o, gate/up, down, LM head;
      * 0 = lyk_hip_step_tile_rows' choice for this device */
     int32_t tile_rows[5];
+    /* lyk_step_model.lds_prefetch: 0 = as many as fit, -1 = none */
+    int32_t lds_prefetch;
 } lyk_model_options;
 
 /* QwenHipModel::Load from a safetensors file (replaces QwenCudaModel::Load,

@@ -369,9 +369,56 @@ def test_batched_long_rows_match_sequential(cuda, long_case, lens):
 
 
 @pytest.mark.parametrize("kw", [dict(attn_split_tokens=24), dict(attn_max_splits=33),
-                                dict(attn_split_tokens=-16), dict(kv_block_tokens=8)],
-                         ids=["tokens_not_tile_multiple", "too_many_splits", "negative", "block_not_16"])
+                                dict(attn_split_tokens=-16), dict(kv_block_tokens=8), dict(lds_prefetch=-2)],
+                         ids=["tokens_not_tile_multiple", "too_many_splits", "negative", "block_not_16",
+                              "bad_lds_prefetch"])
 def test_attention_options_rejected(cuda, kw):
     with pytest.raises(M.ModelError) as e:
         M.HipModel.synthetic(MID, seed=1, options=M.Options(quant="int4", **kw))
     assert e.value.code in (M.UNSUPPORTED_MODEL, M.INVALID_REQUEST)
+
+
+# ------------------------------------------------- gate/up staging in LDS
+def staged_run(cfg, mode, lds_prefetch, rows, seed=3, steps=6):
+    """Logits of a prefill and `steps` greedy batched decode steps of `rows`
+    sequences (prompts of different lengths)."""
+    hip = M.HipModel.synthetic(cfg, seed=seed, sigma=0.02,
+                               options=M.Options(quant=mode, kv_pool_tokens=4096, lds_prefetch=lds_prefetch))
+    seqs = [hip.new_seq(min(cfg.max_context_tokens, 512)) for _ in range(rows)]
+    outs = [hip.prefill(s, list(O.synth_tokens(4, i, 20 + 7 * i, cfg.vocab_size)))[1] for i, s in enumerate(seqs)]
+    got = [np.stack(outs)]
+    for _ in range(steps):
+        toks = [O.argmax(l) for l in outs]
+        if rows == 1:
+            code, l = hip.decode(seqs[0], toks[0])
+            outs = [l]
+        else:
+            code, per, logits = hip.decode_batch(seqs, toks)
+            assert per == [0] * rows
+            outs = list(logits)
+        assert code == 0
+        got.append(np.stack(outs))
+    hip.close()
+    return np.stack(got)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 4])
+@pytest.mark.parametrize("cfg", [MID, MID128], ids=["hd64", "hd128"])
+@pytest.mark.parametrize("mode", MODES)
+def test_lds_staging_is_bit_exact(cuda, cfg, mode, rows):
+    """Staging the gate/up weights in LDS changes where the GEMV reads them
+    from, not the arithmetic: every amount of staging (as many chunks as fit,
+    one, two) gives the logits of none, bit for bit."""
+    base = staged_run(cfg, mode, -1, rows)
+    for pf in (0, 1, 2):
+        got = staged_run(cfg, mode, pf, rows)
+        assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), pf
+
+
+def test_lds_staging_bit_exact_at_7b_shape(cuda):
+    """The same at Qwen2.5-7B geometry (int4), where the staging region holds
+    about half of each wave's gate/up chunks."""
+    cfg = M.QWEN25_7B
+    base = staged_run(cfg, "int4", -1, 1, steps=3)
+    got = staged_run(cfg, "int4", 0, 1, steps=3)
+    assert np.array_equal(got.view(np.uint32), base.view(np.uint32))
