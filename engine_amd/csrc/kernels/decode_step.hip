@@ -112,6 +112,34 @@ __device__ __forceinline__ bool take(const u64* p, uint32_t tag, uint32_t& paylo
 __device__ __forceinline__ uint32_t fbits(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ float bitsf(uint32_t u) { return __builtin_bit_cast(float, u); }
 
+// One attempt at N tagged words. All N loads are issued, unconditionally,
+// before any is tested, so an attempt costs one memory round trip for the
+// whole batch (testing a word before the next load is issued costs a round
+// trip per word). at(u) must give a readable address for every u; word u is
+// wanted when bit u of `want` is set and it has not arrived yet (bit u of
+// `have`), and got(u, payload) takes it on arrival. Returns the wanted
+// words still missing.
+template <int N, class At, class Got>
+__device__ __forceinline__ int poll_batch(uint32_t want, uint32_t& have, uint32_t tag, At at, Got got) {
+    static_assert(N <= 32, "batch");
+    const uint32_t pend = want & ~have;
+    u64 w[N];
+#pragma unroll
+    for (int u = 0; u < N; ++u) w[u] = load_sc1(at(u));
+    int missing = 0;
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+        const bool wanted = pend >> u & 1;
+        const bool hit = (uint32_t)(w[u] >> 32) == tag;
+        if (wanted && hit) {
+            have |= 1u << u;
+            got(u, (uint32_t)w[u]);
+        }
+        missing += wanted && !hit ? 1 : 0;
+    }
+    return missing;
+}
+
 __device__ __forceinline__ bool aborted(const StepArgs& a) { return load_sc1<int>(a.err) != 0; }
 
 // Polls until `pending()` (which re-reads the words still missing and
@@ -475,27 +503,30 @@ template <int M>
 __device__ __forceinline__ bool residual_add(const StepArgs& a, float (&h)[M][kNormPer], const u64* d,
                                              uint32_t tag, int tid) {
     const int H = a.md.hidden_size;
-    uint32_t have[M];   // bit j: element j of row m received
+    // rows in batches of up to two: word u = (j, row m0 + u % RB) of a batch
+    constexpr int RB = M < 2 ? M : 2, NB = (M + RB - 1) / RB;
+    static_assert(kNormPer * 2 <= 32, "residual batch");
+    uint32_t want = 0, have[NB];
 #pragma unroll
-    for (int m = 0; m < M; ++m) have[m] = 0;
+    for (int j = 0; j < kNormPer; ++j)
+        if (tid + j * kThreads < H) want |= ((1u << RB) - 1) << (j * RB);
+#pragma unroll
+    for (int q = 0; q < NB; ++q) have[q] = 0;
     float add[M][kNormPer];
     auto pending = [&]() {
         int missing = 0;
 #pragma unroll
-        for (int j = 0; j < kNormPer; ++j) {
-            const int i = tid + j * kThreads;
-            if (i >= H) continue;
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                if (have[m] >> j & 1) continue;
-                uint32_t u;
-                if (take(d + (size_t)m * H + i, tag, u)) {
-                    add[m][j] = bitsf(u);
-                    have[m] |= 1u << j;
-                } else {
-                    ++missing;
-                }
-            }
+        for (int q = 0; q < NB; ++q) {
+            const int m0 = q * RB;
+            const uint32_t wq = m0 + RB <= M ? want : want & 0x55555555u;   // last batch of odd M: one row
+            missing += poll_batch<kNormPer * RB>(
+                wq, have[q], tag,
+                [&](int u) {
+                    return d + (size_t)min(m0 + u % RB, M - 1) * H + min(tid + (u / RB) * kThreads, H - 1);
+                },
+                [&](int u, uint32_t v) {
+                    if (m0 + u % RB < M) add[m0 + u % RB][u / RB] = bitsf(v);
+                });
         }
         return missing;
     };
@@ -572,23 +603,16 @@ __device__ __forceinline__ bool poll_words(const StepArgs& a, const u64* src, in
     bool ok = true;
     for (int e0 = tid; e0 < n; e0 += kThreads * KB) {
         uint32_t v[KB];
-        uint32_t have = 0;
-        auto pending = [&]() {
-            int missing = 0;
+        uint32_t want = 0, have = 0;
 #pragma unroll
-            for (int u = 0; u < KB; ++u) {
-                const int e = e0 + u * kThreads;
-                if (e >= n || (have >> u & 1)) continue;
-                if (e >= valid) {
-                    v[u] = 0;
-                    have |= 1u << u;
-                } else if (take(src + e, tag, v[u])) {
-                    have |= 1u << u;
-                } else {
-                    ++missing;
-                }
-            }
-            return missing;
+        for (int u = 0; u < KB; ++u) {
+            const int e = e0 + u * kThreads;
+            v[u] = 0;
+            if (e < n && e < valid) want |= 1u << u;
+        }
+        auto pending = [&]() {
+            return poll_batch<KB>(want, have, tag, [&](int u) { return src + min(e0 + u * kThreads, valid - 1); },
+                                  [&](int u, uint32_t x) { v[u] = x; });
         };
         ok = spin(a, pending) && ok;
 #pragma unroll
@@ -889,25 +913,29 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                     put(dpart + (((size_t)t * np + s) * M + m) * 64 + lane, fbits(v[m]), tag);
                 continue;
             }
+            // rows in batches of up to two; word u of a batch: piece
+            // 1 + u / RB, row m0 + u % RB
+            constexpr int RB = M < 2 ? M : 2, NB = (M + RB - 1) / RB;
             float got[kMaxPieces][M];
-            uint32_t have = 0;
+            uint32_t have[NB];
+#pragma unroll
+            for (int q = 0; q < NB; ++q) have[q] = 0;
+            const u64* part = dpart + ((size_t)t * np + 1) * M * 64 + lane;
             auto pending = [&]() {
                 int missing = 0;
 #pragma unroll
-                for (int s2 = 1; s2 < kMaxPieces; ++s2) {
-                    if (s2 >= np) continue;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const int bit = s2 * M + m;
-                        if (have >> bit & 1) continue;
-                        uint32_t u;
-                        if (take(dpart + (((size_t)t * np + s2) * M + m) * 64 + lane, tag, u)) {
-                            got[s2][m] = bitsf(u);
-                            have |= 1u << bit;
-                        } else {
-                            ++missing;
-                        }
-                    }
+                for (int q = 0; q < NB; ++q) {
+                    const int m0 = q * RB, rb = m0 + RB <= M ? RB : M - m0;
+                    uint32_t want = 0;
+                    for (int s2 = 1; s2 < np; ++s2) want |= ((1u << rb) - 1) << ((s2 - 1) * RB);
+                    missing += poll_batch<(kMaxPieces - 1) * RB>(
+                        want, have[q], tag,
+                        [&](int u) {
+                            return part + ((size_t)min(u / RB, np - 2) * M + min(m0 + u % RB, M - 1)) * 64;
+                        },
+                        [&](int u, uint32_t x) {
+                            if (m0 + u % RB < M) got[1 + u / RB][m0 + u % RB] = bitsf(x);
+                        });
                 }
                 return missing;
             };
@@ -1201,7 +1229,6 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
             const int nw = GH + (last ? 2 * HD : 0);
             for (int e0 = tid; e0 < nw; e0 += kThreads * 4) {
                 uint32_t v[4];
-                uint32_t have = 0;
                 int idx[4];
                 float bias[4];
 #pragma unroll
@@ -1211,16 +1238,13 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                                      : (e < GH + HD ? kq + g * HD + (e - GH) : kq + nkv * HD + g * HD + (e - GH - HD));
                     bias[u2] = e < nw ? ld(Lw.qkv_bias + idx[u2]) : 0.0f;
                 }
-                auto pending = [&]() {
-                    int missing = 0;
+                uint32_t want = 0, have = 0;
 #pragma unroll
-                    for (int u2 = 0; u2 < 4; ++u2) {
-                        const int e = e0 + u2 * kThreads;
-                        if (e >= nw || (have >> u2 & 1)) continue;
-                        if (take(src + idx[u2], tag, v[u2])) have |= 1u << u2;
-                        else ++missing;
-                    }
-                    return missing;
+                for (int u2 = 0; u2 < 4; ++u2)
+                    if (e0 + u2 * kThreads < nw) want |= 1u << u2;
+                auto pending = [&]() {
+                    return poll_batch<4>(want, have, tag, [&](int u2) { return src + (want >> u2 & 1 ? idx[u2] : idx[0]); },
+                                         [&](int u2, uint32_t x) { v[u2] = x; });
                 };
                 ok = spin(a, pending) && ok;
 #pragma unroll
@@ -1414,22 +1438,18 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         const int nml = Sm * G * 2, nw = nml + ne * Sm;
         for (int b0 = tid; b0 < nw; b0 += kThreads * 4) {
             uint32_t v[4];
-            uint32_t have = 0;
             auto word = [&](int e) -> const u64* {
                 if (e < nml) return a.attn_ml + (grp * kAttnMaxSplits + e / (2 * G)) * G * 2 + e % (2 * G);
                 const int k = e - nml;
                 return a.attn_acc + (grp * kAttnMaxSplits + k % Sm) * (size_t)GH + e0 + k / Sm;
             };
-            auto pending = [&]() {
-                int missing = 0;
+            uint32_t want = 0, have = 0;
 #pragma unroll
-                for (int u2 = 0; u2 < 4; ++u2) {
-                    const int e = b0 + u2 * kThreads;
-                    if (e >= nw || (have >> u2 & 1)) continue;
-                    if (take(word(e), tag, v[u2])) have |= 1u << u2;
-                    else ++missing;
-                }
-                return missing;
+            for (int u2 = 0; u2 < 4; ++u2)
+                if (b0 + u2 * kThreads < nw) want |= 1u << u2;
+            auto pending = [&]() {
+                return poll_batch<4>(want, have, tag, [&](int u2) { return word(min(b0 + u2 * kThreads, nw - 1)); },
+                                     [&](int u2, uint32_t x) { v[u2] = x; });
             };
             ok = spin(a, pending) && ok;
 #pragma unroll
@@ -1526,14 +1546,8 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
             uint32_t w[3];
             uint32_t have = 0;
             auto pending = [&]() {
-                int missing = 0;
-#pragma unroll
-                for (int k = 0; k < 3; ++k) {
-                    if (have >> k & 1) continue;
-                    if (take(a.best + (size_t)t * 3 + k, htag, w[k])) have |= 1u << k;
-                    else ++missing;
-                }
-                return missing;
+                return poll_batch<3>(7, have, htag, [&](int k) { return a.best + (size_t)t * 3 + k; },
+                                     [&](int k, uint32_t x) { w[k] = x; });
             };
             good = spin(a, pending) && good;
             bst = better(bst, Best{bitsf(w[0]), (int)w[1]});
