@@ -190,6 +190,23 @@ __device__ __forceinline__ void mark(const StepArgs& a, int ph, int kind) {
            (uint64_t)__builtin_amdgcn_s_memrealtime());
 }
 
+// Whether x holds in any thread of the workgroup. (HIP's __syncthreads_or
+// reads the workgroup size from the dispatch packet with a vector load; the
+// wait for it also waits for every load issued before, prefetched weight
+// chunks included.)
+__device__ __forceinline__ bool block_any(bool x) {
+    __shared__ uint32_t votes[kWaves];
+    const int t = threadIdx.x;
+    const bool w = __ballot(x) != 0;
+    if ((t & 63) == 0) votes[t >> 6] = w ? 1u : 0u;
+    __syncthreads();
+    uint32_t r = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) r |= votes[i];
+    __syncthreads();   // the votes are rewritten by the next call
+    return r != 0;
+}
+
 // Sum of v over the workgroup for M rows; every thread gets the sums. Waves
 // are added in wave order.
 template <int M>
@@ -762,7 +779,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     }
     if (g0 + 2 < w1) CM::load(A, g0 + 2, nv_of(g0 + 2), lane, wc, sc);
     if (g0 + 3 < w1) CM::load(A, g0 + 3, nv_of(g0 + 3), lane, wd, sd);
-    if (__syncthreads_or(!ok)) return false;
+    if (block_any(!ok)) return false;
     mark(a, ph, 1);
     if (!p.busy) {
         mark(a, ph, 2);
@@ -1012,7 +1029,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
             }
         }
     }
-    if (__syncthreads_or(!good)) return false;
+    if (block_any(!good)) return false;
     mark(a, ph, 3);
     return true;
 }
@@ -1258,7 +1275,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 }
             }
         }
-        if (__syncthreads_or(!ok)) return false;
+        if (block_any(!ok)) return false;
         // RoPE on q (every head, split into fp16 parts) and on the current
         // key, from the host-built cos/sin tables
         {
@@ -1459,7 +1476,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 else if (e < nw) vals[e - nml] = bitsf(v[u2]);
             }
         }
-        if (__syncthreads_or(!ok)) return false;
+        if (block_any(!ok)) return false;
         // split weights e_s = exp(m_s - max) and the total sum, one wave per
         // head and a lane per split (splits <= 32 < 64)
         for (int h = wave; h < G; h += kWaves) {
@@ -1559,7 +1576,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
             auto pending = [&]() { return load_sc1(a.seq + w) == seq + 1u ? 0 : 1; };
             good = spin(a, pending) && good;
         }
-        if (__syncthreads_or(!good)) return;
+        if (block_any(!good)) return;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) bst = better(bst, Best{__shfl_xor(bst.v, o, 64), __shfl_xor(bst.i, o, 64)});
         bad = (int)wave_sum((float)bad);
