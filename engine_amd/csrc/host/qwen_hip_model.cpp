@@ -501,7 +501,7 @@ struct QwenHipModel::Impl {
 namespace {
 
 Status QuantizeUpload(bool q8, const std::vector<float>& a, const std::vector<float>* b, int64_t n,
-                      int64_t k, int tile_rows, PackedMat& out, uint64_t& bytes) {
+                      int64_t k, bool normed_input, int tile_rows, PackedMat& out, uint64_t& bytes) {
     const int64_t ns = q8 ? 1 : (k + 31) / 32;
     std::vector<int8_t> ca((size_t)(n * k)), cb;
     std::vector<uint16_t> sa((size_t)(n * ns)), sb;
@@ -516,7 +516,7 @@ Status QuantizeUpload(bool q8, const std::vector<float>& a, const std::vector<fl
         if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight quantization failed", kComponent);
     }
     // the tile height the fused step streams this shape best with on this device
-    const int tr = tile_rows ? tile_rows : lyk_hip_step_tile_rows(n, k, b != nullptr, q8 ? 1 : 0);
+    const int tr = tile_rows ? tile_rows : lyk_hip_step_tile_rows(n, k, b != nullptr, q8 ? 1 : 0, normed_input ? 1 : 0);
     if (tr == 0) return Status(ErrorCode::kGpuUnhealthy, "hip device properties unavailable", kComponent);
     if (tr != 16 && tr != 32 && tr != 64) return Status(ErrorCode::kUnsupportedModel, "tile height must be 16, 32 or 64", kComponent);
     uint64_t wb = 0, sbytes = 0;
@@ -628,23 +628,23 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
             LOAD_OR_RETURN(read(LayerName(l, nm), {std::string(nm).find("q_proj") != std::string::npos ? qd : kvd}, t));
             bias.insert(bias.end(), t.begin(), t.end());
         }
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, qkv, nullptr, int64_t(qd + 2 * kvd), int64_t(H), options.tile_rows[0], L.qkv, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, qkv, nullptr, int64_t(qd + 2 * kvd), int64_t(H), true, options.tile_rows[0], L.qkv, I.gemv_bytes));
         LOAD_OR_RETURN(UploadF32(bias, L.qkv_bias));
         LOAD_OR_RETURN(read(LayerName(l, "self_attn.o_proj.weight"), {H, qd}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(qd), options.tile_rows[1], L.o, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(qd), false, options.tile_rows[1], L.o, I.gemv_bytes));
         LOAD_OR_RETURN(read(LayerName(l, "mlp.gate_proj.weight"), {In, H}, a));
         LOAD_OR_RETURN(read(LayerName(l, "mlp.up_proj.weight"), {In, H}, b));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, &b, int64_t(In), int64_t(H), options.tile_rows[2], L.gateup, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, &b, int64_t(In), int64_t(H), true, options.tile_rows[2], L.gateup, I.gemv_bytes));
         LOAD_OR_RETURN(read(LayerName(l, "mlp.down_proj.weight"), {H, In}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(In), options.tile_rows[3], L.down, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(In), false, options.tile_rows[3], L.down, I.gemv_bytes));
     }
     LOAD_OR_RETURN(read("model.norm.weight", {H}, a));
     LOAD_OR_RETURN(UploadF32(a, I.final_norm));
     if (c.tie_word_embeddings) {
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, embed, nullptr, int64_t(V), int64_t(H), options.tile_rows[4], I.lm_head, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, embed, nullptr, int64_t(V), int64_t(H), true, options.tile_rows[4], I.lm_head, I.gemv_bytes));
     } else {
         LOAD_OR_RETURN(read("lm_head.weight", {V, H}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(V), int64_t(H), options.tile_rows[4], I.lm_head, I.gemv_bytes));
+        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(V), int64_t(H), true, options.tile_rows[4], I.lm_head, I.gemv_bytes));
     }
     if (src.tensor_count() != expected) {
         r.status = Status(ErrorCode::kArtifactVerificationFailed, "weight file contains unexpected tensors",

@@ -1615,13 +1615,19 @@ void tiled_shape(int64_t n, int64_t k, bool paired, bool q8, int tr, int64_t& ti
     ck = (int64_t)kChunkBlocks * lpr * unit;
 }
 
-// Tile height for an [n, k] matrix on a grid of `grid` workgroups: the
-// tallest whose busiest workgroup streams at most 15% more chunks than the
-// average busy one (tiles split into K pieces where there are few, each piece
-// polling only its share of the input window); failing that, the one whose
+// Tile height for an [n, k] matrix on a grid of `grid` workgroups.
+// A matrix whose input is the RMSNorm of the residual (QKV, gate/up, LM head)
+// gains nothing from cutting tiles into K pieces (every workgroup holds the
+// whole residual), and each piece costs a merge hop: the height whose busiest
+// workgroup streams the fewest chunks, a merge counted as kMergeChunks more
+// (about the chunks a CU streams in the hop's time), ties to the taller.
+// Otherwise (polled inputs: O, down), the tallest whose busiest workgroup
+// streams at most 15% more chunks than the average busy one (pieces poll
+// only their share of the input window); failing that, the one whose
 // busiest workgroup streams least. Taller tiles also keep a wave's lanes on
 // more rows, so fewer lane sums to combine.
-int choose_tile_rows(int64_t n, int64_t k, bool paired, bool q8, int grid) {
+constexpr int64_t kMergeChunks = 16;
+int choose_tile_rows(int64_t n, int64_t k, bool paired, bool q8, bool normed_input, int grid) {
     int best = 0;
     int64_t best_max = -1;
     for (int tr : {64, 32, 16}) {
@@ -1639,6 +1645,14 @@ int choose_tile_rows(int64_t n, int64_t k, bool paired, bool q8, int grid) {
         // a wave's chunk range may touch at most kPieces tiles
         const int64_t lw = (per_wg + kWaves - 1) / kWaves;
         if (1 + (lw - 1 + chunks - 1) / chunks > kPieces) continue;
+        if (normed_input) {
+            const int64_t cost = per_wg + (pieces > 1 ? kMergeChunks : 0);
+            if (best_max < 0 || cost < best_max) {
+                best = tr;
+                best_max = cost;
+            }
+            continue;
+        }
         const double avg = (double)tiles * chunks / (double)busy;
         if ((double)per_wg <= 1.15 * avg) return tr;
         if (best_max < 0 || per_wg < best_max) {
@@ -1909,10 +1923,10 @@ uint32_t lyk_hip_step_phases(const lyk_step_model* model, int mode) {
 
 int lyk_hip_step_grid(void) { return step_grid(); }
 
-int lyk_hip_step_tile_rows(int64_t n, int64_t k, int paired, int q8) {
+int lyk_hip_step_tile_rows(int64_t n, int64_t k, int paired, int q8, int normed_input) {
     const int grid = step_grid();
     if (n <= 0 || k <= 0 || grid < 1) return 0;
-    return choose_tile_rows(n, k, paired != 0, q8 != 0, grid);
+    return choose_tile_rows(n, k, paired != 0, q8 != 0, normed_input != 0, grid);
 }
 
 int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void* d_workspace,

@@ -66,7 +66,7 @@ _KERNEL_SIGS = {
     "lyk_hip_step_workspace_bytes": (U64, [P, I]),
     "lyk_hip_step_phases": (U32, [P, I]),
     "lyk_hip_step_grid": (I, []),
-    "lyk_hip_step_tile_rows": (I, [I64, I64, I, I]),
+    "lyk_hip_step_tile_rows": (I, [I64, I64, I, I, I]),
     "lyk_hip_decode_step": (I, [P, P, P, U64, I, P]),
     "lyk_hip_step_reset": (I, [P, U64, P]),
     "lyk_hip_step_error": (I, [P, C.POINTER(C.c_int32), P]),

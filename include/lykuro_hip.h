@@ -334,9 +334,10 @@ uint64_t lyk_hip_step_workspace_bytes(const lyk_step_model* model, int max_rows)
 uint32_t lyk_hip_step_phases(const lyk_step_model* model, int mode);
 int lyk_hip_step_grid(void);
 /* Tile height to pack an [n, k] GEMV matrix with for the step on this device
- * (paired: gate/up; q8: int8 weights): the one whose busiest workgroup
- * streams the least; 0 on invalid arguments. */
-int lyk_hip_step_tile_rows(int64_t n, int64_t k, int paired, int q8);
+ * (paired: gate/up; q8: int8 weights; normed_input: the matrix reads the
+ * RMSNorm of the residual, as QKV, gate/up and the LM head do, so cutting
+ * its tiles into K pieces saves no input traffic); 0 on invalid arguments. */
+int lyk_hip_step_tile_rows(int64_t n, int64_t k, int paired, int q8, int normed_input);
 /* Launches one step (stream-ordered, asynchronous). Positions must be
  * < rope_positions and have their blocks in the tables; the host checks
  * both. The launch arguments are kept in the workspace and uploaded only when
