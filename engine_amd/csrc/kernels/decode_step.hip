@@ -63,7 +63,8 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kPieces = 4;           // row tiles one wave's range may touch
 constexpr int kNormPer = 10;         // hidden_size <= kNormPer * kThreads
 constexpr int kMaxRows = 4;
-constexpr int kAttnMaxSplits = 32;   // context splits per (row, kv head), at most
+constexpr int kAttnMaxSplits = 64;   // context splits per (row, kv head), at most (a lane each in the merge)
+constexpr int kAttnDefaultSplits = 32;   // the default cap: more units than the grid has workgroups idle in QKV wait on QKV work
 constexpr int kAttnSplitTokens = 32; // default: tokens per split, at least
 constexpr int kChunkBlocks = 4;      // 16-byte blocks per lane in a GEMV chunk
 constexpr int kMinPieceChunks = 4;   // K chunks per piece of a split tile, at least
@@ -1478,7 +1479,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         }
         if (block_any(!ok)) return false;
         // split weights e_s = exp(m_s - max) and the total sum, one wave per
-        // head and a lane per split (splits <= 32 < 64)
+        // head and a lane per split (splits <= 64)
         for (int h = wave; h < G; h += kWaves) {
             const bool live = lane < Sm;
             const float ms = live ? mlv[(lane * G + h) * 2] : -INFINITY;
@@ -1967,7 +1968,7 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     a.dpart_stride = (size_t)L.dpart_stride;
     a.best = reinterpret_cast<u64*>(ws + L.best);
     a.attn_split_tokens = model->attn_split_tokens ? model->attn_split_tokens : kAttnSplitTokens;
-    a.attn_max_splits = model->attn_max_splits ? model->attn_max_splits : kAttnMaxSplits;
+    a.attn_max_splits = model->attn_max_splits ? model->attn_max_splits : kAttnDefaultSplits;
     a.phases = (int)lyk_hip_step_phases(model, io->mode);
     const Staging sg = gateup_staging(*model, m, grid);
     a.pf_off = sg.off;

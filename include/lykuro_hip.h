@@ -280,7 +280,7 @@ typedef struct lyk_step_model {
     int32_t rope_positions;  /* rows of the cos/sin tables */
     /* Attention split of a row's context over workgroups: equal splits of
      * whole 16-token tiles, at least attn_split_tokens (a multiple of 16) long,
-     * at most attn_max_splits (<= 32) of them; 0 selects the defaults (32, 32). */
+     * at most attn_max_splits (<= 64) of them; 0 selects the defaults (32, 32). */
     int32_t attn_split_tokens, attn_max_splits;
     /* Tile height (16, 32 or 64) each GEMV matrix was packed with
      * (lyk_q*_pack_tiled), in the order qkv, o, gate/up, down, LM head;

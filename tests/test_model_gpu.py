@@ -279,8 +279,10 @@ LONG128 = O.QwenConfig(4096, 896, 2, 7, 1, 128, 2048, 1536, 1e-6, 1e6, True, 409
 LONG_PROMPT, LONG_STEPS = 1100, 6
 # (attn_split_tokens, attn_max_splits): the defaults (many splits merged
 # across workgroups), one split per kv head (a unit runs five 256-token
-# softmax chunks), three splits, and splits of at least 256 tokens.
-POLICIES = {"default": (0, 0), "one_split": (0, 1), "three_splits": (16, 3), "min256": (256, 32)}
+# softmax chunks), three splits, splits of at least 256 tokens, and 35 splits
+# of 32 tokens (more splits than half a wave of lanes in the merge).
+POLICIES = {"default": (0, 0), "one_split": (0, 1), "three_splits": (16, 3), "min256": (256, 32),
+            "split35": (32, 64)}
 
 
 @pytest.fixture(scope="module", params=[LONG64, LONG128], ids=["hd64", "hd128"])
@@ -368,7 +370,7 @@ def test_batched_long_rows_match_sequential(cuda, long_case, lens):
     hip.close()
 
 
-@pytest.mark.parametrize("kw", [dict(attn_split_tokens=24), dict(attn_max_splits=33),
+@pytest.mark.parametrize("kw", [dict(attn_split_tokens=24), dict(attn_max_splits=65),
                                 dict(attn_split_tokens=-16), dict(kv_block_tokens=8), dict(lds_prefetch=-2)],
                          ids=["tokens_not_tile_multiple", "too_many_splits", "negative", "block_not_16",
                               "bad_lds_prefetch"])
