@@ -1,0 +1,289 @@
+// Temperature / top-k / top-p sampling of logits on the device.
+//
+// Reference: Sampler::Sample (core/generation/sampler.cpp:35-106). The rule,
+// restated: non-finite logits fail the row; temperature 0 takes the first
+// index of the maximum; otherwise the indices are stably sorted by logit,
+// descending, and cut to top_k; p_i = exp(double(l_i - l_max) * inv_temp) with
+// inv_temp = 1.0f / temperature (float); the nucleus is the shortest prefix
+// whose running sum of p_i / denom reaches top_p (denom = the sum of the
+// candidates' p_i, in sorted order); r = u * mass (mass = the nucleus's sum),
+// u the draw generate_canonical<double, 53> of the caller's mt19937_64 (what
+// uniform_real_distribution<double>(0, mass) computes); the token is the
+// first of the nucleus whose running sum reaches r.
+//
+// One workgroup per row:
+//   1. scan: non-finite check and the first maximum;
+//   2. candidates: every index whose p_i >= 2^-54, as 64-bit sort keys
+//      (inverted order-preserving logit bits, index) -- a prefix of the
+//      sorted order, and the only terms that can change a running sum that
+//      starts at p_0 = 1: a smaller term is below half an ulp of every sum
+//      the rule forms (each is >= 1, or for the top-p sums >= 1/denom with
+//      the terms divided by denom alike), so adding it rounds back;
+//   3. bitonic sort of the keys (LDS when they fit, else global memory);
+//   4. p_i in parallel, then the rule's three running sums in order by one
+//      lane, in double, as the reference forms them.
+// The result equals the reference's draw for draw; the one difference is
+// the device's double exp, within an ulp of the host's, which moves a token
+// only when r lies within about 1e-16 of a boundary.
+#include <cmath>
+#include <random>
+
+#include "common.h"
+
+namespace lyk {
+namespace {
+
+constexpr int kMaxRows = 4;            // rows per call, at most (the decode batch)
+constexpr int kSampleThreads = 1024;
+constexpr int kLdsKeys = 8192;        // keys sorted in LDS (64 KiB); more go through global memory
+constexpr double kMinTerm = 0x1p-54;  // terms below this never change a running sum
+
+struct Draws {
+    double u[kMaxRows];
+};
+
+__device__ __forceinline__ uint32_t order_bits(float x) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);   // ascending with x
+}
+
+// Whether a term exp(d) reaches kMinTerm (ln 2^-54 = -37.4299...): exp is
+// evaluated only near the cut.
+__device__ __forceinline__ bool significant(double d) {
+    if (d < -37.45) return false;
+    if (d > -37.41) return true;
+    return exp(d) >= kMinTerm;
+}
+
+// Sum over the workgroup of an int, every thread gets it.
+__device__ int block_count(int v, int* scratch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    int s = 0;
+    for (int w = 0; w < kSampleThreads / 64; ++w) s += scratch[w];
+    __syncthreads();
+    return s;
+}
+
+// Exclusive prefix of v over the threads in thread order, and the total.
+__device__ int block_prefix(int v, int* scratch, int& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) scratch[wave] = x;
+    __syncthreads();
+    int base = 0;
+    total = 0;
+    for (int w = 0; w < kSampleThreads / 64; ++w) {
+        if (w < wave) base += scratch[w];
+        total += scratch[w];
+    }
+    __syncthreads();
+    return base + x - v;
+}
+
+// Ascending bitonic sort of a[0..n2) (n2 a power of two) by the workgroup.
+template <class T>
+__device__ void bitonic_sort(T* a, int n2) {
+    for (int k = 2; k <= n2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < n2; i += kSampleThreads) {
+                const int p = i ^ j;
+                if (p > i) {
+                    const bool up = (i & k) == 0;
+                    const T x = a[i], y = a[p];
+                    if ((x > y) == up) {
+                        a[i] = y;
+                        a[p] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __restrict__ logits, int ldl, int n,
+                                                                float temperature, int top_k, float top_p,
+                                                                Draws draws, uint64_t* __restrict__ keys_all,
+                                                                double* __restrict__ probs_all, int cap,
+                                                                int32_t* __restrict__ tokens) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int scratch[kSampleThreads / 64];
+    __shared__ float bmax[kSampleThreads / 64];
+    __shared__ int bidx[kSampleThreads / 64];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* l = logits + (size_t)row * ldl;
+    uint64_t* keys = keys_all + (size_t)row * cap;
+    double* probs = probs_all + (size_t)row * cap;
+
+    // 1. non-finite count and the first maximum
+    float mv = -INFINITY;
+    int mi = 0x7fffffff, bad = 0;
+    for (int i = tid; i < n; i += kSampleThreads) {
+        const float x = l[i];
+        if (!isfinite(x)) {
+            bad = 1;
+            continue;
+        }
+        if (x > mv || (x == mv && i < mi)) {
+            mv = x;
+            mi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(mv, o, 64);
+        const int i2 = __shfl_xor(mi, o, 64);
+        if (v2 > mv || (v2 == mv && i2 < mi)) {
+            mv = v2;
+            mi = i2;
+        }
+    }
+    if ((tid & 63) == 0) {
+        bmax[tid >> 6] = mv;
+        bidx[tid >> 6] = mi;
+    }
+    bad = block_count(bad, scratch);   // its barriers publish bmax / bidx too
+    if (bad) {
+        if (tid == 0) tokens[row] = -1;
+        return;
+    }
+    mv = bmax[0];
+    mi = bidx[0];
+    for (int w = 1; w < kSampleThreads / 64; ++w)
+        if (bmax[w] > mv || (bmax[w] == mv && bidx[w] < mi)) {
+            mv = bmax[w];
+            mi = bidx[w];
+        }
+    if (temperature == 0.0f) {
+        if (tid == 0) tokens[row] = mi;
+        return;
+    }
+
+    // 2. candidates: p_i >= 2^-54, keys (inverted logit order bits, index)
+    const float inv_temp = 1.0f / temperature;
+    int mine = 0;
+    for (int i = tid; i < n; i += kSampleThreads)
+        if (significant((double)(l[i] - mv) * inv_temp)) ++mine;
+    int total;
+    int at = block_prefix(mine, scratch, total);
+    for (int i = tid; i < n; i += kSampleThreads)
+        if (significant((double)(l[i] - mv) * inv_temp))
+            keys[at++] = ((uint64_t)~order_bits(l[i]) << 32) | (uint32_t)i;
+    const int nc = total;   // >= 1: the maximum's term is 1
+
+    // 3. sort ascending: logits descending, equal logits by index
+    int n2 = 1;
+    while (n2 < nc) n2 <<= 1;
+    __syncthreads();
+    if (n2 <= kLdsKeys) {
+        uint64_t* s = reinterpret_cast<uint64_t*>(smem);
+        for (int i = tid; i < n2; i += kSampleThreads) s[i] = i < nc ? keys[i] : ~0ull;
+        __syncthreads();
+        bitonic_sort(s, n2);
+        for (int i = tid; i < nc; i += kSampleThreads) keys[i] = s[i];
+    } else {
+        for (int i = nc + tid; i < n2; i += kSampleThreads) keys[i] = ~0ull;
+        __syncthreads();
+        bitonic_sort(keys, n2);
+    }
+    __syncthreads();
+
+    // 4. terms in parallel; the running sums in order by one lane
+    const int cand = top_k > 0 && top_k < nc ? top_k : nc;
+    for (int i = tid; i < cand; i += kSampleThreads)
+        probs[i] = exp((double)(l[(uint32_t)keys[i]] - mv) * inv_temp);
+    __syncthreads();
+    if (tid != 0) return;
+    double denom = 0.0;
+    for (int i = 0; i < cand; ++i) denom += probs[i];
+    int nucleus = cand;
+    if (top_p < 1.0f) {
+        double cum = 0.0;
+        for (int i = 0; i < cand; ++i) {
+            cum += probs[i] / denom;
+            if (cum >= (double)top_p) {
+                nucleus = i + 1;
+                break;
+            }
+        }
+    }
+    double mass = 0.0;
+    for (int i = 0; i < nucleus; ++i) mass += probs[i];
+    const double r = draws.u[row] * (mass - 0.0) + 0.0;
+    double acc = 0.0;
+    int tok = (int)(uint32_t)keys[nucleus - 1];
+    for (int i = 0; i < nucleus; ++i) {
+        acc += probs[i];
+        if (r <= acc) {
+            tok = (int)(uint32_t)keys[i];
+            break;
+        }
+    }
+    tokens[row] = tok;
+}
+
+}  // namespace
+}  // namespace lyk
+
+using namespace lyk;
+
+extern "C" {
+
+uint64_t lyk_hip_sample_workspace_bytes(int m, int64_t n) {
+    if (m < 1 || n < 1) return 0;
+    int64_t cap = 1;
+    while (cap < n) cap <<= 1;
+    return (uint64_t)m * (uint64_t)cap * 16;
+}
+
+int lyk_hip_sample(const float* d_logits, int64_t ldl, int m, int64_t n, float temperature, int32_t top_k,
+                   float top_p, const double* u, int32_t* d_tokens, void* d_workspace, uint64_t workspace_bytes,
+                   void* stream) {
+    if (!d_logits || !d_tokens || !u || m < 1 || n < 1 || ldl < n || n > (1 << 30)) return LYK_ERR_INVALID_ARG;
+    if (m > kMaxRows) return LYK_ERR_SHAPE;
+    if (!(temperature >= 0.0f) || !std::isfinite(temperature) || !(top_p > 0.0f) || top_p > 1.0f || top_k < 0)
+        return LYK_ERR_INVALID_ARG;
+    if (!d_workspace || workspace_bytes < lyk_hip_sample_workspace_bytes(m, n)) return LYK_ERR_WORKSPACE;
+    Draws d{};
+    for (int r = 0; r < m; ++r) {
+        if (!(u[r] >= 0.0 && u[r] < 1.0)) return LYK_ERR_INVALID_ARG;
+        d.u[r] = u[r];
+    }
+    int cap = 1;
+    while (cap < n) cap <<= 1;
+    char* base = static_cast<char*>(d_workspace);
+    uint64_t* keys = reinterpret_cast<uint64_t*>(base);
+    double* probs = reinterpret_cast<double*>(base + (size_t)m * cap * 8);
+    static bool lds_set = false;
+    if (!lds_set) {
+        if (hipFuncSetAttribute((const void*)sample_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kLdsKeys * 8) != hipSuccess)
+            return LYK_ERR_HIP;
+        lds_set = true;
+    }
+    hipLaunchKernelGGL(sample_kernel, dim3(m), dim3(kSampleThreads), kLdsKeys * 8, (hipStream_t)stream, d_logits,
+                       (int)ldl, (int)n, temperature, top_k, top_p, d, keys, probs, cap, d_tokens);
+    LYK_LAUNCH_CHECK();
+    return LYK_OK;
+}
+
+// The draws Sampler takes from its generator: std::mt19937_64 seeded with
+// the request's seed (sampler.cpp:32-33), one generate_canonical<double, 53>
+// per non-greedy token (what uniform_real_distribution<double>(0, mass)
+// draws before scaling by mass).
+void* lyk_rng_new(uint64_t seed) { return new std::mt19937_64(seed); }
+void lyk_rng_free(void* g) { delete static_cast<std::mt19937_64*>(g); }
+double lyk_rng_canonical(void* g) {
+    return std::generate_canonical<double, 53>(*static_cast<std::mt19937_64*>(g));
+}
+
+}  // extern "C"

@@ -60,6 +60,11 @@ _KERNEL_SIGS = {
     "lyk_hip_attn_decode": (I, [P, P, P, P, I, P, I, I, I, I, I, I, I, P, I64, P, U64, P]),
     "lyk_hip_argmax_workspace_bytes": (U64, [I, I64]),
     "lyk_hip_argmax": (I, [P, I64, I, I64, P, P, P, P, P, P, U64, P]),
+    "lyk_hip_sample_workspace_bytes": (U64, [I, I64]),
+    "lyk_hip_sample": (I, [P, I64, I, I64, C.c_float, C.c_int32, C.c_float, P, P, P, U64, P]),
+    "lyk_rng_new": (P, [U64]),
+    "lyk_rng_free": (None, [P]),
+    "lyk_rng_canonical": (C.c_double, [P]),
     "lyk_hip_gemv_splits": (I, [I64, I64, I, I, I]),
     "lyk_hip_gemv_q4": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),
     "lyk_hip_gemv_q8": (I, [P, P, I64, I64, P, I64, I, I, P, I64, P, I, P, U64, P]),

@@ -147,3 +147,43 @@ def gemv(pw: PackedWeight, x, epilogue=L.EPI_STORE, y=None, bias=None, splits=0,
 def padded_k(k, mode):
     unit = 32 if mode == "int4" else 16
     return (k + unit - 1) // unit * unit
+
+
+class Rng:
+    """The generator Sampler draws from (core/generation/sampler.cpp:32-33):
+    std::mt19937_64 seeded with the request's seed, one
+    generate_canonical<double, 53> per non-greedy token."""
+
+    def __init__(self, seed):
+        self._h = L.kernels().lyk_rng_new(int(seed))
+
+    def canonical(self):
+        return float(L.kernels().lyk_rng_canonical(self._h))
+
+    def close(self):
+        if self._h:
+            L.kernels().lyk_rng_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
+def sample(logits, temperature, top_k, top_p, u, workspace=None):
+    """Device sampling of each row of `logits` ([m, n] fp32 on the GPU),
+    Sampler::Sample's rule with the given draws u (one per row). Returns the
+    tokens as an int32 tensor on the device (-1: a non-finite logit)."""
+    assert logits.dtype == torch.float32 and logits.dim() == 2 and logits.is_cuda
+    m, n = logits.shape
+    ld = logits.stride(0)
+    assert logits.stride(1) == 1 and len(u) == m
+    k = L.kernels()
+    need = k.lyk_hip_sample_workspace_bytes(m, n)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=logits.device)
+    out = torch.empty(m, dtype=torch.int32, device=logits.device)
+    draws = (C.c_double * m)(*u)
+    L.check("lyk_hip_sample", k.lyk_hip_sample(_p(logits), ld, m, n, float(temperature), int(top_k),
+                                                float(top_p), draws, _p(out), _p(workspace), need,
+                                                stream_ptr()))
+    return out

@@ -239,6 +239,28 @@ int lyk_hip_argmax(const float* d_logits, int64_t ldl, int m, int64_t n,
                    int32_t* d_history, int32_t* d_step, void* d_workspace,
                    uint64_t workspace_bytes, void* stream);
 
+/* Temperature / top-k / top-p sampling per row, Sampler::Sample's rule
+ * (core/generation/sampler.cpp:35-106; replaces the host sort the engine runs
+ * on downloaded logits). temperature 0: the first index of the maximum; else
+ * the stable descending order cut to top_k (0 = all), p_i =
+ * exp(double(l_i - l_max) * (1.0f / temperature)), the shortest prefix whose
+ * running sum of p_i / sum reaches top_p, and the first of it whose running
+ * sum reaches u[r] * (its mass). u[r] in [0, 1): the row's draw, one
+ * lyk_rng_canonical per non-greedy token. d_tokens[r] = the token, or -1
+ * when the row holds a non-finite logit (the reference's kInferenceFailed).
+ * m <= 4 rows of ldl floats, one workgroup each. */
+uint64_t lyk_hip_sample_workspace_bytes(int m, int64_t n);
+int lyk_hip_sample(const float* d_logits, int64_t ldl, int m, int64_t n,
+                   float temperature, int32_t top_k, float top_p,
+                   const double* u, int32_t* d_tokens, void* d_workspace,
+                   uint64_t workspace_bytes, void* stream);
+/* The generator Sampler draws from (sampler.cpp:32-33): std::mt19937_64
+ * seeded with the request's seed; lyk_rng_canonical returns the next
+ * generate_canonical<double, 53> draw, the u of lyk_hip_sample. */
+void* lyk_rng_new(uint64_t seed);
+void lyk_rng_free(void* rng);
+double lyk_rng_canonical(void* rng);
+
 /* ---------------------------------------------------- fused decode step
  * One decode step of a Qwen2 model (embedding, every layer, final norm, LM
  * head, greedy argmax) as a single persistent cooperative launch of one
