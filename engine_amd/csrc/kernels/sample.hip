@@ -13,7 +13,10 @@
 //
 // One workgroup per row:
 //   1. scan: non-finite check and the first maximum;
-//   2. candidates: every index whose p_i >= 2^-54, as 64-bit sort keys
+//   2. with top_k, the k-th largest logit by a radix select over the order
+//      bits (four 8-bit digits, LDS histograms), so that only logits at or
+//      above it are kept;
+//      candidates: every kept index whose p_i >= 2^-54, as 64-bit sort keys
 //      (inverted order-preserving logit bits, index) -- a prefix of the
 //      sorted order, and the only terms that can change a running sum that
 //      starts at p_0 = 1: a smaller term is below half an ulp of every sum
@@ -168,16 +171,49 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __r
         return;
     }
 
-    // 2. candidates: p_i >= 2^-54, keys (inverted logit order bits, index)
+    // 2. top_k: the order bits of the k-th largest logit (ties counted
+    //    whole: the sort below cuts them by index)
+    uint32_t floor_bits = 0;
+    if (top_k > 0 && top_k < n) {
+        int* hist = reinterpret_cast<int*>(smem);
+        __shared__ int pick, left;
+        uint32_t prefix = 0, mask = 0;
+        if (tid == 0) left = top_k;
+        for (int d = 3; d >= 0; --d) {
+            for (int b = tid; b < 256; b += kSampleThreads) hist[b] = 0;
+            __syncthreads();
+            for (int i = tid; i < n; i += kSampleThreads) {
+                const uint32_t ob = order_bits(l[i]);
+                if ((ob & mask) == prefix) atomicAdd(&hist[(ob >> (8 * d)) & 255], 1);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int cum = 0, b = 255;
+                for (; b > 0; --b) {
+                    if (cum + hist[b] >= left) break;
+                    cum += hist[b];
+                }
+                pick = b;
+                left -= cum;
+            }
+            __syncthreads();
+            prefix |= (uint32_t)pick << (8 * d);
+            mask |= 255u << (8 * d);
+        }
+        floor_bits = prefix;
+    }
+    // candidates: kept and p_i >= 2^-54, keys (inverted logit order bits, index)
     const float inv_temp = 1.0f / temperature;
+    auto keep = [&](float x) {
+        return order_bits(x) >= floor_bits && significant((double)(x - mv) * inv_temp);
+    };
     int mine = 0;
     for (int i = tid; i < n; i += kSampleThreads)
-        if (significant((double)(l[i] - mv) * inv_temp)) ++mine;
+        if (keep(l[i])) ++mine;
     int total;
     int at = block_prefix(mine, scratch, total);
     for (int i = tid; i < n; i += kSampleThreads)
-        if (significant((double)(l[i] - mv) * inv_temp))
-            keys[at++] = ((uint64_t)~order_bits(l[i]) << 32) | (uint32_t)i;
+        if (keep(l[i])) keys[at++] = ((uint64_t)~order_bits(l[i]) << 32) | (uint32_t)i;
     const int nc = total;   // >= 1: the maximum's term is 1
 
     // 3. sort ascending: logits descending, equal logits by index
