@@ -60,6 +60,7 @@ _KERNEL_SIGS = {
     "lyk_hip_attn_decode": (I, [P, P, P, P, I, P, I, I, I, I, I, I, I, P, I64, P, U64, P]),
     "lyk_hip_argmax_workspace_bytes": (U64, [I, I64]),
     "lyk_hip_argmax": (I, [P, I64, I, I64, P, P, P, P, P, P, U64, P]),
+    "lyk_hip_gemm_q": (I, [P, I64, I64, I64, P, P, I64, I, I, P, P, I64, P]),
     "lyk_hip_sample_workspace_bytes": (U64, [I, I64]),
     "lyk_hip_sample": (I, [P, I64, I, I64, C.c_float, C.c_int32, C.c_float, P, P, P, U64, P]),
     "lyk_rng_new": (P, [U64]),

@@ -187,3 +187,31 @@ def sample(logits, temperature, top_k, top_p, u, workspace=None):
                                                 float(top_p), draws, _p(out), _p(workspace), need,
                                                 stream_ptr()))
     return out
+
+
+def pack_tiled(codes, scales, mode, tile_rows):
+    """The fused step's tiled layout of one (not paired) matrix: (qw, qs) uint8 arrays."""
+    n, k = codes.shape
+    q8 = mode == "int8"
+    wb, sb = C.c_uint64(), C.c_uint64()
+    lay = L.kernels().lyk_q8_layout_tiled if q8 else L.kernels().lyk_q4_layout_tiled
+    L.check("layout_tiled", lay(n, k, 0, tile_rows, C.byref(wb), C.byref(sb)))
+    qw = np.zeros(wb.value, np.uint8)
+    qs = np.zeros(sb.value, np.uint8)
+    pack = L.kernels().lyk_q8_pack_tiled if q8 else L.kernels().lyk_q4_pack_tiled
+    L.check("pack_tiled", pack(_p(np.ascontiguousarray(codes)), _p(np.ascontiguousarray(scales)), None, None,
+                               n, k, tile_rows, _p(qw), _p(qs)))
+    return qw, qs
+
+
+def gemm_q(x, qw, qs, n, mode, tile_rows, bias=None):
+    """Y[T, n] = X . W^T (+ bias) on the matrix cores; x fp16 [T, K] on the GPU
+    (row stride a multiple of 8), qw / qs the tiled layout on the GPU."""
+    assert x.dtype == torch.float16 and x.dim() == 2 and x.stride(1) == 1
+    T, K = x.shape
+    y = torch.empty(T, n, dtype=torch.float32, device=x.device)
+    L.check("lyk_hip_gemm_q", L.kernels().lyk_hip_gemm_q(_p(x), x.stride(0), T, K, _p(qw), _p(qs), n, tile_rows,
+                                                         1 if mode == "int8" else 0,
+                                                         _p(bias) if bias is not None else None, _p(y), n,
+                                                         stream_ptr()))
+    return y

@@ -239,6 +239,16 @@ int lyk_hip_argmax(const float* d_logits, int64_t ldl, int m, int64_t n,
                    int32_t* d_history, int32_t* d_step, void* d_workspace,
                    uint64_t workspace_bytes, void* stream);
 
+/* Prefill GEMM on the matrix cores: d_y[t][j] = sum_k x[t][k] * W[j][k]
+ * (+ d_bias[j]) for t < T, j < n; x fp16 [T][ldx] (ldx a multiple of 8), W
+ * one matrix of n rows (not paired) in the tiled layout above with tile height
+ * tile_rows (q8: int8), y fp32 [T][ldy]. Replaces GemmXWtKernel
+ * (backends/cuda/qwen_cuda_model.cu:878-908), the chunk GEMM of prefill. */
+int lyk_hip_gemm_q(const uint16_t* d_x, int64_t ldx, int64_t T, int64_t K,
+                   const void* d_qw, const void* d_qs, int64_t n, int tile_rows,
+                   int q8, const float* d_bias, float* d_y, int64_t ldy,
+                   void* stream);
+
 /* Temperature / top-k / top-p sampling per row, Sampler::Sample's rule
  * (core/generation/sampler.cpp:35-106; replaces the host sort the engine runs
  * on downloaded logits). temperature 0: the first index of the maximum; else
