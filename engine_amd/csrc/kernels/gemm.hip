@@ -7,16 +7,16 @@
 // prompt rows, in FP32 SIMT tiles there; the CPU path is one MatVec per row
 // (model/architectures/qwen/qwen_model.cpp:21-31).
 //
-// A workgroup (4 waves) computes a 64 x 64 tile of Y: wave w the rows
-// 16w..16w+15, four 16 x 16 accumulators across the 64 columns. Each step of
-// 32 k is one v_mfma_f32_16x16x32_f16 per accumulator:
-//   A: lane l holds X[row l % 16][8 (l / 16) .. +7] (one 16-byte load);
-//   B: lane l holds W[column l % 16][8 (l / 16) .. +7] as exact small
-//      integers q in fp16 (int4: a code's nibble through a magic-number OR;
-//      int8: its byte through v_perm), read straight from the tiled layout.
-// The scales stay out of the matrix product, so it is exact in its inputs:
-// int4 multiplies each group's product by the column's group scale (every
-// 32-k step is one group), int8 the finished sum by the row scale.
+// A workgroup (4 waves) computes a 128 x 128 tile of Y, each wave a 64 x 64
+// quarter as 4 x 4 accumulators of 16 x 16. Per step of 32 k the workgroup
+// stages in LDS the X tile (fp16) and the W tile dequantized to fp16 (int4:
+// code x group scale, rounded to fp16 once; int8: the code, its row scale
+// applied to the finished sum), then each wave runs 16
+// v_mfma_f32_16x16x32_f16 from LDS operands:
+//   A: lane l holds X[row l % 16][8 (l / 16) .. +7];
+//   B: lane l holds W[column l % 16][8 (l / 16) .. +7].
+// fp32 accumulation. (The fp16 rounding of int4 code x scale is the only
+// rounding before the sum: 2^-12 relative per weight.)
 #include "common.h"
 
 namespace lyk {
@@ -26,6 +26,9 @@ constexpr int kGemmThreads = 256;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 128;      // rows and columns of Y per workgroup
+constexpr int kRowHalves = 40;  // LDS row of a 32-k slice (fp16), padded against bank conflicts
 
 __device__ __forceinline__ uint32_t lane_of(int r, int unit, int tr, int& blk) {
     const int per = 64 / tr;   // units a block holds per row
@@ -39,108 +42,118 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
                                                            const uint16_t* __restrict__ qs, int n, int tr, int nbp,
                                                            int nc, const float* __restrict__ bias,
                                                            float* __restrict__ y, int ldy) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __align__(16) uint16_t xs[kTile * kRowHalves];
+    __shared__ __align__(16) uint16_t ws[kTile * kRowHalves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int quad = lane >> 4, col = lane & 15;
-    const int t0 = blockIdx.y * 64 + wave * 16, n0 = blockIdx.x * 64;
-    const int trow = t0 + col;   // this lane's A row
-    f32x4 acc[4];
+    const int t0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;   // this wave's quarter
+    f32x4 acc[4][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // this lane's B column in each accumulator: tile, row in tile
-    int tt[4], rr[4];
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int c = n0 + 16 * j + col;
-        tt[j] = c / tr;
-        rr[j] = c % tr;
-    }
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // staging roles: X row tid / 2, 16 k from 16 (tid & 1); W column tid / 2,
+    // 8 k slices 2 (tid & 1) and 2 (tid & 1) + 1
+    const int xr = tid >> 1, xh = tid & 1;
+    const int wcol = tid >> 1, wd = 2 * (tid & 1);
+    const int cn = n0 + wcol;
+    const int wt = cn / tr, wrr = cn % tr;
+    const half2_t lo_off = {(half_t)-1032.0f, (half_t)-1032.0f};
+    const half2_t hi_off = {(half_t)-1152.0f, (half_t)-1152.0f};
+    const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
     const int steps = (K + 31) / 32;
     for (int g = 0; g < steps; ++g) {
-        // A: X[trow][32g + 8 quad .. +7], zero past T and K
-        const int k0 = 32 * g + 8 * quad;
-        uint32_t av[4] = {0u, 0u, 0u, 0u};
-        if (trow < T) {
-            const uint16_t* xr = x + (size_t)trow * ldx;
-            if (k0 + 8 <= K) {
-                const u32x4 v = ld(reinterpret_cast<const u32x4*>(xr + k0));
-                av[0] = v.x;
-                av[1] = v.y;
-                av[2] = v.z;
-                av[3] = v.w;
-            } else {
-                for (int e = 0; e < 8; ++e)
-                    if (k0 + e < K) av[e / 2] |= (uint32_t)ld(xr + k0 + e) << (16 * (e & 1));
-            }
-        }
-        const f16x8 a = __builtin_bit_cast(f16x8, u32x4{av[0], av[1], av[2], av[3]});
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = n0 + 16 * j + col;
-            uint32_t bv[4] = {0u, 0u, 0u, 0u};
-            float s = 0.0f;
-            if (c < n) {
-                if constexpr (!Q8) {
-                    // unit = group g; the lane's u32 `quad` of it: k 8 quad .. +7
-                    int blk;
-                    const uint32_t l = lane_of(rr[j], g, tr, blk);
-                    const uint32_t u = ld(reinterpret_cast<const uint32_t*>(
-                        qw + (((size_t)tt[j] * nbp + blk) * 64 + l) * 16 + 4 * quad));
-                    const uint32_t t = u >> 8, magic = 0x64006400u;
-                    // nibbles of k 8q+{0,1} | {2,3} (x16) | {4,5} | {6,7} (x16)
-                    const half2_t lo_off = {(half_t)-1032.0f, (half_t)-1032.0f};
-                    const half2_t hi_off = {(half_t)-1152.0f, (half_t)-1152.0f};
-                    const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
-                    const half2_t p0 = as_half2((u & 0x000F000Fu) | magic) + lo_off;
-                    const half2_t p1 = (as_half2((u & 0x00F000F0u) | magic) + hi_off) * sixteenth;
-                    const half2_t p2 = as_half2((t & 0x000F000Fu) | magic) + lo_off;
-                    const half2_t p3 = (as_half2((t & 0x00F000F0u) | magic) + hi_off) * sixteenth;
-                    bv[0] = __builtin_bit_cast(uint32_t, p0);
-                    bv[1] = __builtin_bit_cast(uint32_t, p1);
-                    bv[2] = __builtin_bit_cast(uint32_t, p2);
-                    bv[3] = __builtin_bit_cast(uint32_t, p3);
-                    s = h2f(ld(qs + (((size_t)tt[j] * nc + blk / 4) * 64 + l) * 4 + blk % 4));
+        // ---- stage X[t0 + xr][32g + 16 xh .. +15]
+        {
+            const int t = t0 + xr, k0 = 32 * g + 16 * xh;
+            u32x4 v0 = {0u, 0u, 0u, 0u}, v1 = {0u, 0u, 0u, 0u};
+            if (t < T) {
+                const uint16_t* p = x + (size_t)t * ldx + k0;
+                if (k0 + 16 <= K) {
+                    v0 = ld(reinterpret_cast<const u32x4*>(p));
+                    v1 = ld(reinterpret_cast<const u32x4*>(p + 8));
                 } else {
-                    // units of 16 codes: k 8 quad .. +7 is half (quad & 1) of unit 2g + quad / 2
-                    int blk;
-                    const uint32_t l = lane_of(rr[j], 2 * g + quad / 2, tr, blk);
-                    const uint8_t* p = qw + (((size_t)tt[j] * nbp + blk) * 64 + l) * 16 + 8 * (quad & 1);
-                    const uint32_t w0 = ld(reinterpret_cast<const uint32_t*>(p));
-                    const uint32_t w1 = ld(reinterpret_cast<const uint32_t*>(p + 4));
-                    const half2_t off = {(half_t)-1152.0f, (half_t)-1152.0f};
-                    const uint32_t ws[2] = {w0, w1};
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const half2_t e0 = as_half2(__builtin_amdgcn_perm(0x64646464u, ws[h], 0x04010400u)) + off;
-                        const half2_t e1 = as_half2(__builtin_amdgcn_perm(0x64646464u, ws[h], 0x04030402u)) + off;
-                        bv[2 * h] = __builtin_bit_cast(uint32_t, e0);
-                        bv[2 * h + 1] = __builtin_bit_cast(uint32_t, e1);
-                    }
+                    uint32_t e[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+                    for (int q = 0; q < 16; ++q)
+                        if (k0 + q < K) e[q / 2] |= (uint32_t)ld(p + q) << (16 * (q & 1));
+                    v0 = u32x4{e[0], e[1], e[2], e[3]};
+                    v1 = u32x4{e[4], e[5], e[6], e[7]};
                 }
             }
-            const f16x8 b = __builtin_bit_cast(f16x8, u32x4{bv[0], bv[1], bv[2], bv[3]});
-            const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-            if constexpr (!Q8) {
-                // D lane l: rows 4 quad + i, column l % 16 -- this lane's B column
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[j][i] = fmaf(part[i], s, acc[j][i]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[j][i] += part[i];
-            }
+            u32x4* d = reinterpret_cast<u32x4*>(xs + xr * kRowHalves + 16 * xh);
+            d[0] = v0;
+            d[1] = v1;
         }
+        // ---- stage W[cn][32g + 8 wd .. +15] dequantized
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int dd = wd + h;   // 8-k slice of the step
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (cn < n) {
+                if constexpr (!Q8) {
+                    int blk;
+                    const uint32_t l = lane_of(wrr, g, tr, blk);
+                    const uint32_t u = ld(reinterpret_cast<const uint32_t*>(
+                        qw + (((size_t)wt * nbp + blk) * 64 + l) * 16 + 4 * dd));
+                    const _Float16 sc = (_Float16)h2f(ld(qs + (((size_t)wt * nc + blk / 4) * 64 + l) * 4 + blk % 4));
+                    const half2_t s2 = {sc, sc};
+                    const uint32_t tt = u >> 8, magic = 0x64006400u;
+                    // nibbles of k 8dd+{0,1} | {2,3} (x16) | {4,5} | {6,7} (x16)
+                    const half2_t p0 = (as_half2((u & 0x000F000Fu) | magic) + lo_off) * s2;
+                    const half2_t p1 = ((as_half2((u & 0x00F000F0u) | magic) + hi_off) * sixteenth) * s2;
+                    const half2_t p2 = (as_half2((tt & 0x000F000Fu) | magic) + lo_off) * s2;
+                    const half2_t p3 = ((as_half2((tt & 0x00F000F0u) | magic) + hi_off) * sixteenth) * s2;
+                    v = u32x4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+                } else {
+                    // 16-code units: slice dd is half (dd & 1) of unit 2g + dd / 2
+                    int blk;
+                    const uint32_t l = lane_of(wrr, 2 * g + dd / 2, tr, blk);
+                    const uint8_t* p = qw + (((size_t)wt * nbp + blk) * 64 + l) * 16 + 8 * (dd & 1);
+                    const uint32_t w2[2] = {ld(reinterpret_cast<const uint32_t*>(p)),
+                                            ld(reinterpret_cast<const uint32_t*>(p + 4))};
+                    uint32_t e[4];
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        e[2 * q] = as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, w2[q], 0x04010400u)) + hi_off);
+                        e[2 * q + 1] =
+                            as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, w2[q], 0x04030402u)) + hi_off);
+                    }
+                    v = u32x4{e[0], e[1], e[2], e[3]};
+                }
+            }
+            *reinterpret_cast<u32x4*>(ws + wcol * kRowHalves + 8 * dd) = v;
+        }
+        __syncthreads();
+        // ---- 16 MFMAs from LDS
+        f16x8 a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            a[i] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(xs + (wr + 16 * i + col) * kRowHalves + 8 * quad));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            b[j] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(ws + (wc + 16 * j + col) * kRowHalves + 8 * quad));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        __syncthreads();   // the tiles are restaged by the next step
     }
+    // D lane l: rows 4 quad + e of the subtile, column l % 16
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int c = n0 + 16 * j + col;
+        const int c = n0 + wc + 16 * j + col;
         if (c >= n) continue;
         float s = 1.0f;
-        if constexpr (Q8) s = h2f(ld(qs + (size_t)tt[j] * 64 + rr[j]));
+        if constexpr (Q8) s = h2f(ld(qs + (size_t)(c / tr) * 64 + c % tr));
         const float bb = bias ? ld(bias + c) : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = t0 + 4 * quad + i;
-            if (t < T) y[(size_t)t * ldy + c] = acc[j][i] * s + bb;
-        }
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = t0 + wr + 16 * i + 4 * quad + e;
+                if (t < T) y[(size_t)t * ldy + c] = acc[i][j][e] * s + bb;
+            }
     }
 }
 
@@ -160,7 +173,7 @@ int lyk_hip_gemm_q(const uint16_t* d_x, int64_t ldx, int64_t T, int64_t K, const
     const int64_t unit = q8 ? 16 : 32, per = 64 / tile_rows;
     const int64_t units = (K + unit - 1) / unit;
     const int64_t nb = (units + per - 1) / per, nc = (nb + 3) / 4, nbp = 4 * nc;
-    dim3 grid((unsigned)((n + 63) / 64), (unsigned)((T + 63) / 64));
+    dim3 grid((unsigned)((n + kTile - 1) / kTile), (unsigned)((T + kTile - 1) / kTile));
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (q8)
         hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kGemmThreads), 0, st, d_x, (int)ldx, (int)T, (int)K,
