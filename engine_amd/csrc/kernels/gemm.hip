@@ -11,7 +11,8 @@
 // quarter as 4 x 4 accumulators of 16 x 16. Per step of 32 k the workgroup
 // stages in LDS the X tile (fp16) and the W tile dequantized to fp16 (int4:
 // code x group scale, rounded to fp16 once; int8: the code, its row scale
-// applied to the finished sum), then each wave runs 16
+// applied to the finished sum; the next step's global words are fetched into
+// registers while this step's MFMAs run), then each wave runs 16
 // v_mfma_f32_16x16x32_f16 from LDS operands:
 //   A: lane l holds X[row l % 16][8 (l / 16) .. +7];
 //   B: lane l holds W[column l % 16][8 (l / 16) .. +7].
@@ -63,68 +64,85 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
     const half2_t hi_off = {(half_t)-1152.0f, (half_t)-1152.0f};
     const half2_t sixteenth = {(half_t)0.0625f, (half_t)0.0625f};
     const int steps = (K + 31) / 32;
-    for (int g = 0; g < steps; ++g) {
-        // ---- stage X[t0 + xr][32g + 16 xh .. +15]
-        {
-            const int t = t0 + xr, k0 = 32 * g + 16 * xh;
-            u32x4 v0 = {0u, 0u, 0u, 0u}, v1 = {0u, 0u, 0u, 0u};
-            if (t < T) {
-                const uint16_t* p = x + (size_t)t * ldx + k0;
-                if (k0 + 16 <= K) {
-                    v0 = ld(reinterpret_cast<const u32x4*>(p));
-                    v1 = ld(reinterpret_cast<const u32x4*>(p + 8));
-                } else {
-                    uint32_t e[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-                    for (int q = 0; q < 16; ++q)
-                        if (k0 + q < K) e[q / 2] |= (uint32_t)ld(p + q) << (16 * (q & 1));
-                    v0 = u32x4{e[0], e[1], e[2], e[3]};
-                    v1 = u32x4{e[4], e[5], e[6], e[7]};
-                }
+    // step g's global words, fetched one step ahead so the loads fly while
+    // the previous step's MFMAs run: X row slice, W words and scale
+    u32x4 xv0, xv1;
+    uint32_t wv[2][2];
+    uint16_t wsc = 0;
+    auto fetch = [&](int g) {
+        const int t = t0 + xr, k0 = 32 * g + 16 * xh;
+        xv0 = u32x4{0u, 0u, 0u, 0u};
+        xv1 = u32x4{0u, 0u, 0u, 0u};
+        if (t < T) {
+            const uint16_t* p = x + (size_t)t * ldx + k0;
+            if (k0 + 16 <= K) {
+                xv0 = ld(reinterpret_cast<const u32x4*>(p));
+                xv1 = ld(reinterpret_cast<const u32x4*>(p + 8));
+            } else {
+                uint32_t e[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+                for (int q = 0; q < 16; ++q)
+                    if (k0 + q < K) e[q / 2] |= (uint32_t)ld(p + q) << (16 * (q & 1));
+                xv0 = u32x4{e[0], e[1], e[2], e[3]};
+                xv1 = u32x4{e[4], e[5], e[6], e[7]};
             }
-            u32x4* d = reinterpret_cast<u32x4*>(xs + xr * kRowHalves + 16 * xh);
-            d[0] = v0;
-            d[1] = v1;
         }
-        // ---- stage W[cn][32g + 8 wd .. +15] dequantized
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int dd = wd + h;   // 8-k slice of the step
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (cn < n) {
-                if constexpr (!Q8) {
-                    int blk;
-                    const uint32_t l = lane_of(wrr, g, tr, blk);
-                    const uint32_t u = ld(reinterpret_cast<const uint32_t*>(
-                        qw + (((size_t)wt * nbp + blk) * 64 + l) * 16 + 4 * dd));
-                    const _Float16 sc = (_Float16)h2f(ld(qs + (((size_t)wt * nc + blk / 4) * 64 + l) * 4 + blk % 4));
-                    const half2_t s2 = {sc, sc};
-                    const uint32_t tt = u >> 8, magic = 0x64006400u;
-                    // nibbles of k 8dd+{0,1} | {2,3} (x16) | {4,5} | {6,7} (x16)
-                    const half2_t p0 = (as_half2((u & 0x000F000Fu) | magic) + lo_off) * s2;
-                    const half2_t p1 = ((as_half2((u & 0x00F000F0u) | magic) + hi_off) * sixteenth) * s2;
-                    const half2_t p2 = (as_half2((tt & 0x000F000Fu) | magic) + lo_off) * s2;
-                    const half2_t p3 = ((as_half2((tt & 0x00F000F0u) | magic) + hi_off) * sixteenth) * s2;
-                    v = u32x4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
-                } else {
-                    // 16-code units: slice dd is half (dd & 1) of unit 2g + dd / 2
-                    int blk;
-                    const uint32_t l = lane_of(wrr, 2 * g + dd / 2, tr, blk);
-                    const uint8_t* p = qw + (((size_t)wt * nbp + blk) * 64 + l) * 16 + 8 * (dd & 1);
-                    const uint32_t w2[2] = {ld(reinterpret_cast<const uint32_t*>(p)),
-                                            ld(reinterpret_cast<const uint32_t*>(p + 4))};
-                    uint32_t e[4];
-#pragma unroll
-                    for (int q = 0; q < 2; ++q) {
-                        e[2 * q] = as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, w2[q], 0x04010400u)) + hi_off);
-                        e[2 * q + 1] =
-                            as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, w2[q], 0x04030402u)) + hi_off);
-                    }
-                    v = u32x4{e[0], e[1], e[2], e[3]};
-                }
+            wv[h][0] = wv[h][1] = 0u;
+            if (cn >= n) continue;
+            if constexpr (!Q8) {
+                int blk;
+                const uint32_t l = lane_of(wrr, g, tr, blk);
+                wv[h][0] = ld(reinterpret_cast<const uint32_t*>(qw + (((size_t)wt * nbp + blk) * 64 + l) * 16 + 4 * dd));
+                if (h == 0) wsc = ld(qs + (((size_t)wt * nc + blk / 4) * 64 + l) * 4 + blk % 4);
+            } else {
+                // 16-code units: slice dd is half (dd & 1) of unit 2g + dd / 2
+                int blk;
+                const uint32_t l = lane_of(wrr, 2 * g + dd / 2, tr, blk);
+                const uint8_t* p = qw + (((size_t)wt * nbp + blk) * 64 + l) * 16 + 8 * (dd & 1);
+                wv[h][0] = ld(reinterpret_cast<const uint32_t*>(p));
+                wv[h][1] = ld(reinterpret_cast<const uint32_t*>(p + 4));
             }
+        }
+    };
+    // the fetched words into LDS: X as is, W dequantized
+    auto stage = [&]() {
+        u32x4* d = reinterpret_cast<u32x4*>(xs + xr * kRowHalves + 16 * xh);
+        d[0] = xv0;
+        d[1] = xv1;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int dd = wd + h;
+            u32x4 v;
+            if constexpr (!Q8) {
+                const _Float16 sc = (_Float16)h2f(wsc);
+                const half2_t s2 = {sc, sc};
+                const uint32_t u = wv[h][0], tt = u >> 8, magic = 0x64006400u;
+                // nibbles of k 8dd+{0,1} | {2,3} (x16) | {4,5} | {6,7} (x16)
+                const half2_t p0 = (as_half2((u & 0x000F000Fu) | magic) + lo_off) * s2;
+                const half2_t p1 = ((as_half2((u & 0x00F000F0u) | magic) + hi_off) * sixteenth) * s2;
+                const half2_t p2 = (as_half2((tt & 0x000F000Fu) | magic) + lo_off) * s2;
+                const half2_t p3 = ((as_half2((tt & 0x00F000F0u) | magic) + hi_off) * sixteenth) * s2;
+                v = u32x4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+            } else {
+                uint32_t e[4];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    e[2 * q] = as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, wv[h][q], 0x04010400u)) + hi_off);
+                    e[2 * q + 1] = as_u32(as_half2(__builtin_amdgcn_perm(0x64646464u, wv[h][q], 0x04030402u)) + hi_off);
+                }
+                v = u32x4{e[0], e[1], e[2], e[3]};
+            }
+            if (cn >= n) v = u32x4{0u, 0u, 0u, 0u};
             *reinterpret_cast<u32x4*>(ws + wcol * kRowHalves + 8 * dd) = v;
         }
+    };
+    fetch(0);
+    for (int g = 0; g < steps; ++g) {
+        stage();
         __syncthreads();
+        if (g + 1 < steps) fetch(g + 1);
         // ---- 16 MFMAs from LDS
         f16x8 a[4], b[4];
 #pragma unroll
