@@ -187,6 +187,38 @@ def cpu_baseline(tokens=3):
                         f"{t_token:.2f}s per token"))
 
 
+def prefill_gemm(quant):
+    """Times the prefill GEMM (lyk_hip_gemm_q) on the 7B gate projection of a
+    2048-token chunk, Y[2048, 18944] = X[2048, 3584] . W^T, and prints one JSON
+    line (not the decode bench line): MFMA TFLOP/s against the fp16 dense peak."""
+    import numpy as np
+    import torch
+    from engine_amd import ops
+    T, n, k, tr = 2048, 18944, 3584, 32
+    w = (np.random.default_rng(0).standard_normal((n, k)) * 0.02).astype(np.float32)
+    codes, scales = ops.quantize(w, quant)
+    qw, qs = ops.pack_tiled(codes, scales, quant, tr)
+    qw, qs = torch.from_numpy(qw).cuda(), torch.from_numpy(qs).cuda()
+    x = torch.randn(T, k, dtype=torch.float16, device="cuda")
+    for _ in range(3):
+        ops.gemm_q(x, qw, qs, n, quant, tr)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 20
+    e0.record()
+    for _ in range(reps):
+        ops.gemm_q(x, qw, qs, n, quant, tr)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    tflops = 2.0 * T * n * k / (us * 1e-6) / 1e12
+    print(json.dumps({"metric": "prefill GEMM TFLOP/s (7B gate projection, 2048-token chunk)", "value": round(tflops, 1),
+                      "unit": "TFLOP/s", "us_per_call": round(us, 1), "quant": quant,
+                      "shape": {"T": T, "n": n, "k": k, "tile_rows": tr},
+                      "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                                   "frac": round(tflops / 2500.0, 4)}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -196,6 +228,7 @@ def main():
     ap.add_argument("--quant", choices=["int4", "int8"], default="int4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--prefill-gemm", action="store_true", help="time the prefill GEMM instead (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -206,6 +239,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.prefill_gemm:
+        prefill_gemm(args.quant)
         return
     dec = run_decode(args)
     achieved = dec["step_bytes"] / (dec["kernel_us"] * 1e-6) / 1e9
