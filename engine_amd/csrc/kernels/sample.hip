@@ -22,9 +22,11 @@
 //      starts at p_0 = 1: a smaller term is below half an ulp of every sum
 //      the rule forms (each is >= 1, or for the top-p sums >= 1/denom with
 //      the terms divided by denom alike), so adding it rounds back;
-//   3. bitonic sort of the keys (LDS when they fit, else global memory);
-//   4. p_i in parallel, then the rule's three running sums in order by one
-//      lane, in double, as the reference forms them.
+//   3. sort of the keys: bitonic in LDS when they fit, else a stable radix
+//      sort in global memory;
+//   4. p_i in parallel, then the rule's three running sums in order (by
+//      wave 0, all lanes carrying the same sums), in double, as the
+//      reference forms them.
 // The result equals the reference's draw for draw; the one difference is
 // the device's double exp, within an ulp of the host's, which moves a token
 // only when r lies within about 1e-16 of a boundary.
@@ -49,6 +51,8 @@ __device__ __forceinline__ uint32_t order_bits(float x) {
     const uint32_t b = __builtin_bit_cast(uint32_t, x);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);   // ascending with x
 }
+
+__device__ __forceinline__ int wave_of(int tid) { return tid >> 6; }
 
 // Whether a term exp(d) reaches kMinTerm (ln 2^-54 = -37.4299...): exp is
 // evaluated only near the cut.
@@ -113,6 +117,65 @@ __device__ void bitonic_sort(T* a, int n2) {
     }
 }
 
+// Stable LSD radix sort of keys[0..n) by their upper 32 bits, 4 bits a pass
+// (8 passes), through tmp; equal upper halves keep their input order, and
+// the result ends in keys. Each pass: digit histogram, bases, then tiles of
+// one key per thread scattered in order (rank within the tile from wave
+// ballots and per-wave counts).
+__device__ void radix_sort_hi(uint64_t* keys, uint64_t* tmp, int n, int* sh) {
+    constexpr int W = kSampleThreads / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int* hist = sh;        // [16]
+    int* base = sh + 16;   // [16] next output slot per digit
+    int* wcnt = sh + 32;   // [W][16] keys per digit in each wave of the tile
+    uint64_t* src = keys;
+    uint64_t* dst = tmp;
+    const uint64_t lt = (1ull << lane) - 1;
+    for (int pass = 0; pass < 8; ++pass) {
+        const int shift = 32 + 4 * pass;
+        if (tid < 16) hist[tid] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += kSampleThreads) atomicAdd(&hist[(int)(src[i] >> shift) & 15], 1);
+        __syncthreads();
+        if (tid == 0) {
+            int acc = 0;
+            for (int d = 0; d < 16; ++d) {
+                base[d] = acc;
+                acc += hist[d];
+            }
+        }
+        __syncthreads();
+        for (int t0 = 0; t0 < n; t0 += kSampleThreads) {
+            const int i = t0 + tid;
+            const bool live = i < n;
+            const uint64_t key = live ? src[i] : 0ull;
+            const int d = live ? (int)(key >> shift) & 15 : -1;
+            int rank = 0;
+            for (int dv = 0; dv < 16; ++dv) {
+                const uint64_t m = __ballot(d == dv);
+                if (d == dv) rank = __popcll(m & lt);
+                if (lane == 0) wcnt[wave * 16 + dv] = __popcll(m);
+            }
+            __syncthreads();
+            if (live) {
+                int off = base[d] + rank;
+                for (int w = 0; w < wave; ++w) off += wcnt[w * 16 + d];
+                dst[off] = key;
+            }
+            __syncthreads();
+            if (tid < 16) {
+                int c = 0;
+                for (int w = 0; w < W; ++w) c += wcnt[w * 16 + tid];
+                base[tid] += c;
+            }
+            __syncthreads();
+        }
+        uint64_t* sw = src;
+        src = dst;
+        dst = sw;
+    }
+}
+
 __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __restrict__ logits, int ldl, int n,
                                                                 float temperature, int top_k, float top_p,
                                                                 Draws draws, uint64_t* __restrict__ keys_all,
@@ -120,6 +183,7 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __r
                                                                 int32_t* __restrict__ tokens) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int scratch[kSampleThreads / 64];
+    __shared__ int sort_sh[32 + 16 * (kSampleThreads / 64)];
     __shared__ float bmax[kSampleThreads / 64];
     __shared__ int bidx[kSampleThreads / 64];
     const int row = blockIdx.x, tid = threadIdx.x;
@@ -207,12 +271,16 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __r
     auto keep = [&](float x) {
         return order_bits(x) >= floor_bits && significant((double)(x - mv) * inv_temp);
     };
+    // each thread a contiguous index range, so the keys come out in index
+    // order (the radix sort below is stable)
+    const int per = (n + kSampleThreads - 1) / kSampleThreads;
+    const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
     int mine = 0;
-    for (int i = tid; i < n; i += kSampleThreads)
+    for (int i = i0; i < i1; ++i)
         if (keep(l[i])) ++mine;
     int total;
     int at = block_prefix(mine, scratch, total);
-    for (int i = tid; i < n; i += kSampleThreads)
+    for (int i = i0; i < i1; ++i)
         if (keep(l[i])) keys[at++] = ((uint64_t)~order_bits(l[i]) << 32) | (uint32_t)i;
     const int nc = total;   // >= 1: the maximum's term is 1
 
@@ -227,43 +295,67 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __r
         bitonic_sort(s, n2);
         for (int i = tid; i < nc; i += kSampleThreads) keys[i] = s[i];
     } else {
-        for (int i = nc + tid; i < n2; i += kSampleThreads) keys[i] = ~0ull;
-        __syncthreads();
-        bitonic_sort(keys, n2);
+        // by logit only: the keys are in index order and the sort is stable
+        radix_sort_hi(keys, reinterpret_cast<uint64_t*>(probs), nc, sort_sh);
     }
     __syncthreads();
 
-    // 4. terms in parallel; the running sums in order by one lane
+    // 4. terms in parallel; the running sums in order by wave 0: a batch of
+    //    64 terms comes in one coalesced load, and every lane adds the batch's
+    //    terms one by one (read across lanes in order), so all lanes carry the
+    //    sequential sum; a term past the end reads 0, which changes no sum
     const int cand = top_k > 0 && top_k < nc ? top_k : nc;
     for (int i = tid; i < cand; i += kSampleThreads)
         probs[i] = exp((double)(l[(uint32_t)keys[i]] - mv) * inv_temp);
     __syncthreads();
-    if (tid != 0) return;
+    if (wave_of(tid) != 0) return;
+    const int lane = tid & 63;
+    auto term = [&](int i, int end) { return i < end ? probs[i] : 0.0; };
     double denom = 0.0;
-    for (int i = 0; i < cand; ++i) denom += probs[i];
+    for (int i0 = 0; i0 < cand; i0 += 64) {
+        const double v = term(i0 + lane, cand);
+#pragma unroll
+        for (int j = 0; j < 64; ++j) denom += __shfl(v, j, 64);
+    }
     int nucleus = cand;
     if (top_p < 1.0f) {
         double cum = 0.0;
-        for (int i = 0; i < cand; ++i) {
-            cum += probs[i] / denom;
-            if (cum >= (double)top_p) {
-                nucleus = i + 1;
-                break;
+        bool found = false;
+        for (int i0 = 0; i0 < cand && !found; i0 += 64) {
+            const double q = term(i0 + lane, cand) / denom;
+#pragma unroll
+            for (int j = 0; j < 64; ++j) {
+                cum += __shfl(q, j, 64);
+                if (!found && i0 + j < cand && cum >= (double)top_p) {
+                    nucleus = i0 + j + 1;
+                    found = true;
+                }
             }
         }
     }
     double mass = 0.0;
-    for (int i = 0; i < nucleus; ++i) mass += probs[i];
+    for (int i0 = 0; i0 < nucleus; i0 += 64) {
+        const double v = term(i0 + lane, nucleus);
+#pragma unroll
+        for (int j = 0; j < 64; ++j) mass += __shfl(v, j, 64);
+    }
     const double r = draws.u[row] * (mass - 0.0) + 0.0;
     double acc = 0.0;
-    int tok = (int)(uint32_t)keys[nucleus - 1];
-    for (int i = 0; i < nucleus; ++i) {
-        acc += probs[i];
-        if (r <= acc) {
-            tok = (int)(uint32_t)keys[i];
-            break;
+    int pick = nucleus - 1;
+    bool found = false;
+    for (int i0 = 0; i0 < nucleus && !found; i0 += 64) {
+        const double v = term(i0 + lane, nucleus);
+#pragma unroll
+        for (int j = 0; j < 64; ++j) {
+            acc += __shfl(v, j, 64);
+            if (!found && i0 + j < nucleus && r <= acc) {
+                pick = i0 + j;
+                found = true;
+            }
         }
     }
+    const int tok = (int)(uint32_t)keys[pick];
+    if (lane != 0) return;
     tokens[row] = tok;
 }
 
