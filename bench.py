@@ -219,6 +219,42 @@ def prefill_gemm(quant):
                                    "frac": round(tflops / 2500.0, 4)}}), flush=True)
 
 
+def sample_bench():
+    """Times device sampling (lyk_hip_sample) of one 152064-logit row, with
+    and without top_k, and the oracle's C restatement of the host Sampler on
+    the same logits (one core) beside it; prints one JSON line."""
+    import numpy as np
+    import torch
+    from engine_amd import lib as L, ops
+    n = 152064
+    logits = (np.random.default_rng(0).standard_normal(n) * 2.5).astype(np.float32)
+    x = torch.from_numpy(logits).reshape(1, -1).cuda()
+    ws = torch.empty(L.kernels().lyk_hip_sample_workspace_bytes(1, n), dtype=torch.uint8, device="cuda")
+    out = {}
+    for name, (t, k, p) in {"top_k40_p0.95_T1": (1.0, 40, 0.95), "p0.9_T0.7": (0.7, 0, 0.9)}.items():
+        for _ in range(3):
+            ops.sample(x, t, k, p, [0.5], ws)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            ops.sample(x, t, k, p, [0.5], ws)
+        e1.record()
+        torch.cuda.synchronize()
+        gpu_us = e0.elapsed_time(e1) * 1e3 / 10
+        from oracle import oracle as O   # the CPU baseline leg
+        sm = O.Sampler(t, p, k, 1)
+        t0 = time.time()
+        for _ in range(3):
+            sm.sample(logits)
+        cpu_us = (time.time() - t0) / 3 * 1e6
+        out[name] = {"gpu_us": round(gpu_us, 1), "cpu_baseline_us": round(cpu_us, 1)}
+    print(json.dumps({"metric": "device sampling latency, V=152064 (model-like logits, N(0, 2.5))", "unit": "us",
+                      "cases": out, "cpu_baseline": {"kind": "port", "cores": 1,
+                                                     "sample": "oracle C restatement of Sampler::Sample"}}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -229,6 +265,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--prefill-gemm", action="store_true", help="time the prefill GEMM instead (one JSON line)")
+    ap.add_argument("--sample", action="store_true", help="time device sampling instead (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -242,6 +279,9 @@ def main():
         return
     if args.prefill_gemm:
         prefill_gemm(args.quant)
+        return
+    if args.sample:
+        sample_bench()
         return
     dec = run_decode(args)
     achieved = dec["step_bytes"] / (dec["kernel_us"] * 1e-6) / 1e9
