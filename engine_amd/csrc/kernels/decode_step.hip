@@ -917,12 +917,23 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         float v[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) v[m] = 0.0f;
+        // every wave's slot read first (independent LDS reads, issued
+        // together), then the in-range ones added in wave order
+        float x[kWaves][M];
+        bool in[kWaves];
+#pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             const int tf = span[w][0], tl = span[w][1];
-            if (t < tf || t > tl) continue;
+            in[w] = t >= tf && t <= tl;
+            const int q = min(max(t - tf, 0), kPieces - 1);
 #pragma unroll
-            for (int m = 0; m < M; ++m) v[m] += red[((w * kPieces + (t - tf)) * M + m) * 64 + lane];
+            for (int m = 0; m < M; ++m) x[w][m] = red[((w * kPieces + q) * M + m) * 64 + lane];
         }
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+            if (in[w])
+#pragma unroll
+                for (int m = 0; m < M; ++m) v[m] += x[w][m];
         if (p.pieces > 1) {
             const int np = p.pieces, s = b % np;
             if (s > 0) {
