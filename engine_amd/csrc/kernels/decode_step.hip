@@ -1571,16 +1571,27 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
         Best bst{-INFINITY, 0x7fffffff};
         int bad = 0;
         bool good = true;
-        for (int t = tid; t < tiles; t += kThreads) {
-            uint32_t w[3];
-            uint32_t have = 0;
+        // four tiles' candidates per thread per round trip
+        constexpr int TB = 4;
+        for (int t0 = tid; t0 < tiles; t0 += kThreads * TB) {
+            uint32_t w[TB * 3];
+            uint32_t want = 0, have = 0;
+#pragma unroll
+            for (int q = 0; q < TB; ++q)
+                if (t0 + q * kThreads < tiles) want |= 7u << (3 * q);
             auto pending = [&]() {
-                return poll_batch<3>(7, have, htag, [&](int k) { return a.best + (size_t)t * 3 + k; },
-                                     [&](int k, uint32_t x) { w[k] = x; });
+                return poll_batch<TB * 3>(
+                    want, have, htag,
+                    [&](int u) { return a.best + (size_t)min(t0 + (u / 3) * kThreads, tiles - 1) * 3 + u % 3; },
+                    [&](int u, uint32_t x) { w[u] = x; });
             };
             good = spin(a, pending) && good;
-            bst = better(bst, Best{bitsf(w[0]), (int)w[1]});
-            bad += (int)w[2];
+#pragma unroll
+            for (int q = 0; q < TB; ++q)
+                if (t0 + q * kThreads < tiles) {
+                    bst = better(bst, Best{bitsf(w[3 * q]), (int)w[3 * q + 1]});
+                    bad += (int)w[3 * q + 2];
+                }
         }
         // The token and position change only after every other workgroup
         // has finished this launch (and so read them).
