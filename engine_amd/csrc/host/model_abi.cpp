@@ -92,6 +92,22 @@ void* lyk_model_load_synthetic(const lyk_model_config* config, uint64_t seed, fl
     return Finish(QwenHipModel::Load(ToManifest(*config), src, ToOptions(options)), status);
 }
 
+int32_t lyk_model_read_tensor_f32(const char* path, const char* name, float* out, uint64_t max_count,
+                                  uint64_t* count) {
+    if (!path || !name) return int32_t(ErrorCode::kInvalidRequest);
+    SafetensorsFile file;
+    Status s = file.Open(path);
+    if (!s.ok()) return Code(s);
+    const TensorInfo* info = file.FindTensor(name);
+    if (info == nullptr) return int32_t(ErrorCode::kArtifactVerificationFailed);
+    std::vector<float> v;
+    s = SafetensorsWeightSource(file).Read(name, info->shape, v);
+    if (!s.ok()) return Code(s);
+    if (count) *count = v.size();
+    if (out) std::memcpy(out, v.data(), std::min<uint64_t>(max_count, v.size()) * 4);
+    return 0;
+}
+
 void lyk_model_free(void* model) { delete M(model); }
 
 void* lyk_model_seq_new(void* model, uint32_t max_tokens, int32_t allow_prefix_cache,
@@ -167,6 +183,13 @@ uint64_t lyk_model_gemv_weight_bytes(const void* model) {
 void* lyk_model_stream(void* model) { return M(model)->stream(); }
 int32_t lyk_model_set_step_tracing(void* model, int32_t on) {
     return Code(M(model)->SetStepTracing(on != 0));
+}
+void lyk_model_set_wait_limit(void* model, uint32_t microseconds) { M(model)->SetWaitLimit(microseconds); }
+uint64_t lyk_model_step_launches(const void* model) {
+    return static_cast<const QwenHipModel*>(model)->step_launches();
+}
+int32_t lyk_model_set_step_launches(void* model, uint64_t launches) {
+    return Code(M(model)->SetStepLaunches(launches));
 }
 size_t lyk_model_step_trace(void* model, uint64_t* out, size_t max) {
     std::vector<uint64_t> t;

@@ -21,6 +21,7 @@
 #include <unordered_map>
 
 #include "fp16.h"
+#include "kv_pool.h"
 #include "lykuro_hip.h"
 #include "lykuro_hip_model.h"
 
@@ -126,132 +127,51 @@ struct PackedMat {
     int tile_rows = 64;   // tiled layout height (lyk_q*_pack_tiled)
 };
 
-// FNV-1a 64, the prefix-cache chain hash (qwen_cuda_model.cu:1623-1630).
-uint64_t Fnv64(uint64_t h, const void* data, size_t len) {
-    const uint8_t* p = static_cast<const uint8_t*>(data);
-    for (size_t i = 0; i < len; ++i) {
-        h ^= p[i];
-        h *= 1099511628211ULL;
-    }
-    return h;
-}
-
-// Block pool shared by every sequence of the model: refcounted blocks, a
-// free list, and prefix-cached blocks that stay resident (evictable, LRU)
-// after their last user releases them. Block ids index every layer's pool.
-class KvPool {
-public:
-    void Init(uint32_t num_blocks, uint32_t block_tokens) {
-        block_tokens_ = block_tokens;
-        meta_.assign(num_blocks, Meta{});
-        free_.clear();
-        for (uint32_t b = 0; b < num_blocks; ++b) free_.push_back(int(num_blocks - 1 - b));
-        by_hash_.clear();
-    }
-    uint32_t block_tokens() const { return block_tokens_; }
-    uint32_t num_blocks() const { return uint32_t(meta_.size()); }
-    uint32_t free_blocks() const {
-        uint32_t evictable = 0;
-        for (const Meta& m : meta_) evictable += (m.cached && m.refs == 0);
-        return uint32_t(free_.size()) + evictable;
-    }
-    bool Allocate(int& out) {
-        if (!free_.empty()) {
-            out = free_.back();
-            free_.pop_back();
-            meta_[out] = Meta{};
-            meta_[out].refs = 1;
-            return true;
-        }
-        int victim = -1;
-        uint64_t oldest = UINT64_MAX;
-        for (uint32_t b = 0; b < meta_.size(); ++b)
-            if (meta_[b].cached && meta_[b].refs == 0 && meta_[b].tick < oldest) {
-                oldest = meta_[b].tick;
-                victim = int(b);
-            }
-        if (victim < 0) return false;
-        by_hash_.erase(meta_[victim].hash);
-        meta_[victim] = Meta{};
-        meta_[victim].refs = 1;
-        out = victim;
-        return true;
-    }
-    void Release(int b) {
-        Meta& m = meta_[b];
-        if (m.refs > 0) --m.refs;
-        if (m.refs == 0) {
-            if (m.cached) m.tick = ++tick_;
-            else free_.push_back(b);
-        }
-    }
-    bool Lookup(uint64_t hash, int& out) {
-        auto it = by_hash_.find(hash);
-        if (it == by_hash_.end()) return false;
-        out = it->second;
-        ++meta_[out].refs;
-        meta_[out].tick = ++tick_;
-        return true;
-    }
-    void Register(uint64_t hash, int b) {
-        if (by_hash_.count(hash) || meta_[b].cached) return;  // first writer wins
-        meta_[b].cached = true;
-        meta_[b].hash = hash;
-        meta_[b].tick = ++tick_;
-        by_hash_.emplace(hash, b);
-    }
-
-private:
-    struct Meta {
-        int refs = 0;
-        bool cached = false;
-        uint64_t hash = 0;
-        uint64_t tick = 0;
-    };
-    uint32_t block_tokens_ = 16;
-    std::vector<Meta> meta_;
-    std::vector<int> free_;
-    std::unordered_map<uint64_t, int> by_hash_;
-    uint64_t tick_ = 0;
-};
-
-// Holds a reference to the pool, so destroying a sequence after its model is
-// still safe; blocks go back to the pool on destruction.
+// A sequence's KV blocks and length. It shares ownership of the pool, so a
+// sequence may outlive its model; its blocks go back to the pool when it is
+// destroyed or cleared.
 class HipSequenceState final : public SequenceState {
 public:
-    HipSequenceState(std::shared_ptr<KvPool> pool, uint32_t max_tokens, SequenceOptions options)
+    HipSequenceState(std::shared_ptr<hip::KvBlockPool> pool, uint32_t max_tokens, SequenceOptions options)
         : pool_(std::move(pool)), max_tokens_(max_tokens), options_(std::move(options)) {}
-    ~HipSequenceState() override {
-        for (int b : blocks_) pool_->Release(b);
-    }
+    ~HipSequenceState() override { Clear(); }
     uint32_t length() const override { return length_; }
     uint32_t capacity() const override { return max_tokens_; }
     const SequenceOptions& options() const { return options_; }
-    const std::vector<int>& blocks() const { return blocks_; }
+    const std::vector<int32_t>& blocks() const { return blocks_; }
 
-    // Blocks for positions [0, pos]; capacity_exhausted when the pool is dry.
-    Status EnsureBlocks(uint32_t pos) {
-        const uint32_t need = pos / pool_->block_tokens() + 1;
-        while (blocks_.size() < need) {
-            int b = -1;
-            if (!pool_->Allocate(b))
-                return Status(ErrorCode::kCapacityExhausted, "kv block pool exhausted", kComponent);
-            blocks_.push_back(b);
+    // Blocks for the first `tokens` positions (capacity_exhausted when the
+    // pool has none left; blocks taken so far are kept).
+    Status Reserve(uint32_t tokens) {
+        const uint32_t bt = pool_->block_tokens();
+        while (size_t(blocks_.size()) * bt < tokens) {
+            const std::optional<int32_t> b = pool_->Take();
+            if (!b) return Status(ErrorCode::kCapacityExhausted, "kv block pool exhausted", kComponent);
+            blocks_.push_back(*b);
         }
         return Status::Ok();
     }
-    void AttachPrefix(std::vector<int> shared, uint32_t tokens) {
-        blocks_ = std::move(shared);
+    // Starts from cached blocks (each already holding a reference for this
+    // sequence) that cover the first `tokens` positions.
+    void Adopt(std::vector<int32_t> cached, uint32_t tokens) {
+        Clear();
+        blocks_ = std::move(cached);
         length_ = tokens;
     }
-    void Advance(uint32_t n = 1) { length_ += n; }
+    // Back to an empty sequence.
+    void Clear() {
+        for (int32_t b : blocks_) pool_->Drop(b);
+        blocks_.clear();
+        length_ = 0;
+    }
+    void Advance(uint32_t n) { length_ += n; }
 
 private:
-    std::shared_ptr<KvPool> pool_;
+    std::shared_ptr<hip::KvBlockPool> pool_;
     uint32_t max_tokens_;
     uint32_t length_ = 0;
     SequenceOptions options_;
-    std::vector<int> blocks_;
+    std::vector<int32_t> blocks_;
 };
 
 // Tensor kinds of the synthetic generator's stream ids (kind*1000 + layer).
@@ -379,8 +299,7 @@ struct QwenHipModel::Impl {
     PackedMat lm_head;
     std::vector<Layer> layers;
 
-    std::shared_ptr<KvPool> pool_ref = std::make_shared<KvPool>();
-    KvPool& pool = *pool_ref;
+    std::shared_ptr<hip::KvBlockPool> pool;
     DevBuf kv;  // [layer][K|V][num_blocks][nkv][bt][hd] fp16
     size_t kv_layer_elems = 0;
 
@@ -433,7 +352,7 @@ struct QwenHipModel::Impl {
         md.rope_cos = rcos.as<float>();
         md.rope_sin = rsin.as<float>();
         md.rope_positions = int32_t(cap);
-        table_stride = std::max<uint32_t>(1, (cap + pool.block_tokens() - 1) / pool.block_tokens());
+        table_stride = std::max<uint32_t>(1, (cap + pool->block_tokens() - 1) / pool->block_tokens());
         s = d_tables.Alloc((size_t)kMaxBatch * table_stride * 4);
         if (!s.ok()) return s;
         return h_tables.Alloc((size_t)kMaxBatch * table_stride * 4);
@@ -659,7 +578,7 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
     const uint64_t pool_tokens =
         options.kv_pool_tokens ? options.kv_pool_tokens : uint64_t(std::max(1u, c.max_context_tokens)) * 4;
     const uint32_t nblocks = uint32_t(std::max<uint64_t>(1, (pool_tokens + bt - 1) / bt));
-    I.pool.Init(nblocks, bt);
+    I.pool = std::make_shared<hip::KvBlockPool>(nblocks, bt);
     I.kv_layer_elems = (size_t)nblocks * c.num_kv_heads * bt * c.head_dim;
     LOAD_OR_RETURN(I.kv.Alloc(I.kv_layer_elems * 2 * 2 * c.num_layers));
 
@@ -773,8 +692,21 @@ Status QwenHipModel::StepTrace(std::vector<uint64_t>& ticks) {
     return Status::Ok();
 }
 
-uint32_t QwenHipModel::kv_blocks_total() const { return impl_->pool.num_blocks(); }
-uint32_t QwenHipModel::kv_blocks_free() const { return impl_->pool.free_blocks(); }
+uint64_t QwenHipModel::step_launches() const { return lyk_hip_step_launches(impl_->d_step_ws.p); }
+
+Status QwenHipModel::SetStepLaunches(uint64_t launches) {
+    HIP_OK(hipSetDevice(device_id_), "hip device not usable");
+    Impl& I = *impl_;
+    HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+    LYK_OK_OR(lyk_hip_step_set_launches(&I.md, kMaxBatch, I.d_step_ws.p, I.step_ws_bytes, launches, I.stream),
+              "step launch count update failed");
+    return Status::Ok();
+}
+
+void QwenHipModel::SetWaitLimit(uint32_t microseconds) { impl_->md.wait_limit_us = microseconds; }
+
+uint32_t QwenHipModel::kv_blocks_total() const { return impl_->pool->num_blocks(); }
+uint32_t QwenHipModel::kv_blocks_free() const { return impl_->pool->available(); }
 uint64_t QwenHipModel::prefix_cache_hit_tokens() const { return impl_->prefix_hits; }
 uint64_t QwenHipModel::gemv_weight_bytes() const { return impl_->gemv_bytes; }
 
@@ -789,7 +721,7 @@ Status QwenHipModel::CreateSequenceEx(uint32_t max_tokens, const SequenceOptions
     HIP_OK(hipSetDevice(device_id_), "hip device not usable");
     Status s = impl_->EnsureRope(std::max(1u, max_tokens));
     if (!s.ok()) return s;
-    out = std::make_unique<HipSequenceState>(impl_->pool_ref, max_tokens, options);
+    out = std::make_unique<HipSequenceState>(impl_->pool, max_tokens, options);
     return Status::Ok();
 }
 
@@ -804,83 +736,73 @@ Status QwenHipModel::Prefill(SequenceState& state, const std::vector<uint32_t>& 
         if (t >= config_.vocab_size) return Status(ErrorCode::kInvalidRequest, "token id out of vocab range", kComponent);
     HIP_OK(hipSetDevice(device_id_), "hip device not usable");
     Impl& I = *impl_;
-    const uint32_t bt = I.pool.block_tokens();
+    const uint32_t bt = I.pool->block_tokens();
     const uint32_t n = uint32_t(tokens.size());
 
-    // Prefix cache: chain hashes seeded with the scope key; the block holding
-    // the last prompt token is never attached, so its logits are computed.
-    std::vector<uint64_t> hashes;
+    // Prefix cache: blocks published under the same scope-seeded chain keys
+    // are adopted from the start of the prompt; the block holding the last
+    // token is always recomputed, so its logits come out.
+    std::vector<uint64_t> keys;
     uint32_t start = 0;
     if (seq.options().allow_prefix_cache) {
-        uint64_t h = 1469598103934665603ULL;
-        h = Fnv64(h, seq.options().scope_key.data(), seq.options().scope_key.size());
-        const uint32_t max_attach = (n - 1) / bt, full = n / bt;
-        std::vector<int> attached;
-        for (uint32_t b = 0; b < full; ++b) {
-            h = Fnv64(h, tokens.data() + size_t(b) * bt, bt * sizeof(uint32_t));
-            hashes.push_back(h);
-            int blk = -1;
-            if (b < max_attach && attached.size() == b && I.pool.Lookup(h, blk)) attached.push_back(blk);
+        keys = hip::PrefixChainKeys(seq.options().scope_key, tokens.data(), n, bt);
+        std::vector<int32_t> hit;
+        for (uint32_t b = 0; b < (n - 1) / bt; ++b) {
+            const std::optional<int32_t> blk = I.pool->Find(keys[b]);
+            if (!blk) break;
+            hit.push_back(*blk);
         }
-        if (!attached.empty()) {
-            start = uint32_t(attached.size()) * bt;
-            seq.AttachPrefix(std::move(attached), start);
-            I.prefix_hits += start;
-        }
+        start = uint32_t(hit.size()) * bt;
+        if (!hit.empty()) seq.Adopt(std::move(hit), start);
     }
+    // Any failure from here leaves the sequence empty again, with nothing
+    // published, so the caller may retry or drop it.
+    auto fail = [&seq](Status s) {
+        seq.Clear();
+        return s;
+    };
 
-    if (start < n) {
-        Status s = seq.EnsureBlocks(n - 1);
-        if (!s.ok()) return s;
-        // Tokens and positions of the whole prompt go up in one copy; each
-        // step then takes its row with a device-to-device copy, so no host
-        // staging buffer is rewritten while a copy from it may be pending.
-        const size_t rows = n - start;
-        if (rows * 2 > I.prompt_cap) {
-            HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
-            I.prompt_cap = std::max<size_t>(rows * 2, 1024);
-            s = I.d_prompt.Alloc(I.prompt_cap * 4);
-            if (!s.ok()) return s;
-            s = I.h_prompt.Alloc(I.prompt_cap * 4);
-            if (!s.ok()) return s;
-        }
-        int32_t* hp = I.h_prompt.as<int32_t>();
-        for (size_t r = 0; r < rows; ++r) {
-            hp[2 * r] = int32_t(tokens[start + r]);
-            hp[2 * r + 1] = int32_t(start + r);
-        }
-        HIP_OK(hipMemcpyAsync(I.d_prompt.p, hp, rows * 8, hipMemcpyHostToDevice, I.stream),
-               "prompt upload failed");
-        s = I.UploadRows({&seq}, {tokens[start]}, {start});
-        if (!s.ok()) return s;
-        for (uint32_t i = start; i < n; ++i) {
-            const int32_t* row = I.d_prompt.as<int32_t>() + 2 * size_t(i - start);
-            HIP_OK(hipMemcpyAsync(I.d_tokens.p, row, 4, hipMemcpyDeviceToDevice, I.stream),
-                   "token copy failed");
-            HIP_OK(hipMemcpyAsync(I.d_pos.p, row + 1, 4, hipMemcpyDeviceToDevice, I.stream),
-                   "position copy failed");
-            const bool last = i + 1 == n;
-            s = I.LaunchStep(1, last ? LYK_STEP_LOGITS : LYK_STEP_HIDDEN);
-            if (!s.ok()) return s;
-        }
-        seq.Advance(n - start);
+    Status s = seq.Reserve(n);
+    if (!s.ok()) return fail(s);
+    // Tokens and positions of the uncached part go up in one copy; each
+    // step takes its row with a device-to-device copy, so no host staging
+    // buffer is rewritten while a copy from it may be pending.
+    const size_t rows = n - start;
+    if (rows * 2 > I.prompt_cap) {
+        HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
+        I.prompt_cap = std::max<size_t>(rows * 2, 1024);
+        if (!(s = I.d_prompt.Alloc(I.prompt_cap * 4)).ok()) return fail(s);
+        if (!(s = I.h_prompt.Alloc(I.prompt_cap * 4)).ok()) return fail(s);
+    }
+    int32_t* hp = I.h_prompt.as<int32_t>();
+    for (size_t r = 0; r < rows; ++r) {
+        hp[2 * r] = int32_t(tokens[start + r]);
+        hp[2 * r + 1] = int32_t(start + r);
+    }
+    if (hipMemcpyAsync(I.d_prompt.p, hp, rows * 8, hipMemcpyHostToDevice, I.stream) != hipSuccess)
+        return fail(Status(ErrorCode::kGpuUnhealthy, "prompt upload failed", kComponent));
+    if (!(s = I.UploadRows({&seq}, {tokens[start]}, {start})).ok()) return fail(s);
+    for (uint32_t i = start; i < n; ++i) {
+        const int32_t* row = I.d_prompt.as<int32_t>() + 2 * size_t(i - start);
+        if (hipMemcpyAsync(I.d_tokens.p, row, 4, hipMemcpyDeviceToDevice, I.stream) != hipSuccess ||
+            hipMemcpyAsync(I.d_pos.p, row + 1, 4, hipMemcpyDeviceToDevice, I.stream) != hipSuccess)
+            return fail(Status(ErrorCode::kGpuUnhealthy, "prompt row copy failed", kComponent));
+        if (!(s = I.LaunchStep(1, i + 1 == n ? LYK_STEP_LOGITS : LYK_STEP_HIDDEN)).ok()) return fail(s);
     }
     logits.resize(config_.vocab_size);
-    HIP_OK(hipMemcpyAsync(I.h_logits.p, I.d_logits.p, logits.size() * 4, hipMemcpyDeviceToHost, I.stream),
-           "logits download failed");
-    HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
-    {
-        Status st = I.CheckSteps();
-        if (!st.ok()) return st;
-    }
+    if (hipMemcpyAsync(I.h_logits.p, I.d_logits.p, logits.size() * 4, hipMemcpyDeviceToHost, I.stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(I.stream) != hipSuccess)
+        return fail(Status(ErrorCode::kGpuUnhealthy, "device execution failed", kComponent));
+    if (!(s = I.CheckSteps()).ok()) return fail(s);
     std::memcpy(logits.data(), I.h_logits.p, logits.size() * 4);
-
-    if (seq.options().allow_prefix_cache)
-        for (uint32_t b = 0; b < hashes.size() && b < seq.blocks().size(); ++b)
-            I.pool.Register(hashes[b], seq.blocks()[b]);
     for (float v : logits)
         if (!std::isfinite(v))
-            return Status(ErrorCode::kInferenceFailed, "logits contain non-finite values", kComponent);
+            return fail(Status(ErrorCode::kInferenceFailed, "logits contain non-finite values", kComponent));
+
+    seq.Advance(n - start);
+    I.prefix_hits += start;
+    for (size_t b = 0; b < keys.size() && b < seq.blocks().size(); ++b) I.pool->Publish(keys[b], seq.blocks()[b]);
     return Status::Ok();
 }
 
@@ -904,11 +826,15 @@ Status QwenHipModel::DecodeBatch(std::vector<DecodeBatchItem>& items, std::vecto
         } else if (st->length() >= st->capacity()) {
             per_item[i] = Status(ErrorCode::kContextLengthExceeded, "kv cache capacity exhausted", kComponent);
         } else {
-            Status cap = st->EnsureBlocks(st->length());
+            Status cap = st->Reserve(st->length() + 1);
             if (!cap.ok()) per_item[i] = cap;
             else valid.push_back(i);
         }
     }
+    // Every group of rows runs before any sequence advances: a device
+    // failure in a later group returns with no sequence advanced (the K/V
+    // rows already written sit past each sequence's length and are
+    // rewritten by its next step).
     const size_t V = config_.vocab_size;
     for (size_t g0 = 0; g0 < valid.size(); g0 += kMaxBatch) {
         const size_t m = std::min<size_t>(kMaxBatch, valid.size() - g0);
@@ -931,21 +857,14 @@ Status QwenHipModel::DecodeBatch(std::vector<DecodeBatchItem>& items, std::vecto
         s = I.CheckSteps();
         if (!s.ok()) return s;
         const float* hl = I.h_logits.as<float>();
-        for (size_t i = 0; i < m; ++i) {
-            const size_t idx = valid[g0 + i];
-            std::vector<float>& out = *items[idx].logits;
-            out.assign(hl + i * V, hl + (i + 1) * V);
-            bool finite = true;
-            for (float v : out)
-                if (!std::isfinite(v)) {
-                    finite = false;
-                    break;
-                }
-            if (!finite)
-                per_item[idx] = Status(ErrorCode::kInferenceFailed, "logits contain non-finite values", kComponent);
-            else
-                seqs[i]->Advance();
-        }
+        for (size_t i = 0; i < m; ++i) items[valid[g0 + i]].logits->assign(hl + i * V, hl + (i + 1) * V);
+    }
+    for (size_t idx : valid) {
+        const std::vector<float>& out = *items[idx].logits;
+        if (std::all_of(out.begin(), out.end(), [](float v) { return std::isfinite(v); }))
+            static_cast<HipSequenceState*>(items[idx].state)->Advance(1);
+        else
+            per_item[idx] = Status(ErrorCode::kInferenceFailed, "logits contain non-finite values", kComponent);
     }
     return Status::Ok();
 }
@@ -963,7 +882,7 @@ Status QwenHipModel::GreedyRun(SequenceState& state, uint32_t token, uint32_t ma
     Impl& I = *impl_;
     const uint32_t len = seq.length();
     const uint32_t steps = std::min({max_new, kGreedyMax, seq.capacity() - len});
-    Status s = seq.EnsureBlocks(len + steps - 1);
+    Status s = seq.Reserve(len + steps);
     if (!s.ok()) return s;
     s = I.UploadRows({&seq}, {token}, {len});
     if (!s.ok()) return s;

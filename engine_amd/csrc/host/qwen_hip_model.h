@@ -152,6 +152,14 @@ public:
     // The HIP stream (hipStream_t) all device work of the model runs on.
     void* stream() const;
     Status StepTrace(std::vector<uint64_t>& ticks);
+    // Launches of the fused step since its workspace was last zeroed, and a
+    // way to preset that count (tests of the launch-tag epoch; see
+    // lyk_hip_step_set_launches).
+    uint64_t step_launches() const;
+    Status SetStepLaunches(uint64_t launches);
+    // Limit of a step's waits for other workgroups (microseconds, 0 = 2 s);
+    // past it the step ends unfinished and the call reports kGpuUnhealthy.
+    void SetWaitLimit(uint32_t microseconds);
 
     struct Impl;
 

@@ -25,6 +25,11 @@ constexpr const char kComponent[] = "safetensors";
 
 Status Bad(const char* msg) { return Status(ErrorCode::kArtifactVerificationFailed, msg, kComponent); }
 
+// Limits on untrusted headers: tensor rank, tensor count, name length.
+constexpr size_t kRankLimit = 8;
+constexpr size_t kTensorLimit = 100000;
+constexpr size_t kNameLimit = 512;
+
 // Minimal JSON reader over the header: objects, arrays, strings (with the
 // escapes JSON allows) and non-negative integers.
 class Json {
@@ -187,6 +192,10 @@ HeaderParseResult ParseSafetensorsHeader(std::string_view text, uint64_t data_se
                 r.status = Bad("duplicate tensor name");
                 return r;
             }
+            if (name.empty() || name.size() > kNameLimit || r.header.tensors.size() >= kTensorLimit) {
+                r.status = Bad("tensor name or count out of range");
+                return r;
+            }
             TensorInfo info;
             bool have_dtype = false, have_shape = false, have_offsets = false;
             std::vector<uint64_t> offsets;
@@ -208,7 +217,7 @@ HeaderParseResult ParseSafetensorsHeader(std::string_view text, uint64_t data_se
                     }
                     have_dtype = true;
                 } else if (key == "shape" && !have_shape) {
-                    if (!j.UintArray(info.shape)) {
+                    if (!j.UintArray(info.shape) || info.shape.size() > kRankLimit) {
                         r.status = Bad("malformed tensor shape");
                         return r;
                     }
@@ -253,6 +262,10 @@ HeaderParseResult ParseSafetensorsHeader(std::string_view text, uint64_t data_se
     }
     if (!j.End()) {
         r.status = Bad("trailing bytes after safetensors header");
+        return r;
+    }
+    if (r.header.tensors.empty()) {
+        r.status = Bad("safetensors file holds no tensors");
         return r;
     }
     std::sort(spans.begin(), spans.end());
@@ -302,10 +315,16 @@ void SafetensorsFile::Close() {
 
 Status SafetensorsFile::Open(const std::string& path, uint64_t max_header_bytes) {
     Close();
-    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    // A symlink is refused (O_NOFOLLOW), and so is anything but a regular
+    // file (a FIFO or device would block or lie about its size).
+    const int fd = ::open(path.c_str(), O_RDONLY | O_NOFOLLOW | O_CLOEXEC | O_NONBLOCK);
     if (fd < 0) return Status(ErrorCode::kArtifactVerificationFailed, "cannot open weight file", kComponent);
     struct stat st;
-    if (fstat(fd, &st) != 0 || st.st_size < 8) {
+    if (fstat(fd, &st) != 0 || !S_ISREG(st.st_mode)) {
+        ::close(fd);
+        return Bad("weight file is not a regular file");
+    }
+    if (st.st_size < 8) {
         ::close(fd);
         return Bad("weight file too small");
     }

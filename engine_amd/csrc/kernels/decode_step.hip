@@ -50,6 +50,7 @@
 #include <mutex>
 #include <type_traits>
 #include <unordered_map>
+#include <vector>
 
 #include "common.h"
 
@@ -69,7 +70,7 @@ constexpr int kAttnSplitTokens = 32; // default: tokens per split, at least
 constexpr int kChunkBlocks = 4;      // 16-byte blocks per lane in a GEMV chunk
 constexpr int kMinPieceChunks = 4;   // K chunks per piece of a split tile, at least
 constexpr int kMaxPieces = 8;        // pieces per split tile, at most
-constexpr uint64_t kSpinTicks = 200000000ull;  // s_memrealtime is 100 MHz: 2 s
+constexpr uint64_t kSpinTicks = 200000000ull;  // default wait limit; s_memrealtime is 100 MHz: 2 s
 constexpr size_t kMaxDynamicLds = 158 * 1024;   // of gfx950's 160 KiB per workgroup; the rest is static
 // Batches of up to kFoldRows rows fold the int4/int8 code offsets out of the
 // GEMV inner loop (a per-unit correction table beside the x window); wider
@@ -96,6 +97,7 @@ struct StepArgs {
     int phases;             // phases of one launch (trace layout)
     int pf_off;             // LDS byte offset of the gate/up staging region
     int pf_chunks;          // gate/up chunks per wave staged there (0: none)
+    uint64_t spin_ticks;    // a wait gives up after this many s_memrealtime ticks
 };
 
 // ------------------------------------------------------------ primitives
@@ -154,13 +156,11 @@ __device__ __forceinline__ bool spin(const StepArgs& a, F pending) {
     for (int it = 1;; ++it) {
         __builtin_amdgcn_s_sleep(2);
         if (pending() == 0) return true;
-        if ((it & 15) == 0) {
-            if (aborted(a)) return false;
-            if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
-                store_sc1(a.err, 1);
-                return false;
-            }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > a.spin_ticks) {
+            store_sc1(a.err, 1);
+            return false;
         }
+        if ((it & 15) == 0 && aborted(a)) return false;
     }
 }
 
@@ -342,26 +342,28 @@ struct ChunkMath<M, false> {
                           : u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
         s = reinterpret_cast<const u64*>(slot + kChunkBlocks * 1024)[lane];
     }
-    // One group (32 codes) against x[32]: four independent dot2 chains.
-    // One group (32 codes) against x[32]. A code's low nibble reads as fp16
-    // 1024 + (q+8) and a high nibble as 1024 + 16(q+8) (one AND/OR each);
-    // their dot products with x carry the offsets, which the group's
-    // correction (1032 * sum of x at the low-nibble positions + 72 * sum at
-    // the high ones, computed once per x window) removes. Four independent
-    // dot2 chains.
-    // (Unfolded, for wide batches: the offsets come off each code first.)
-    __device__ __forceinline__ static float group(const u32x4& w, const u32x4* xv, uint32_t vmagic, float corr) {
+    // One group (32 codes) against x[32]. A code's nibble c = q + 8 becomes
+    // the fp16 subnormal c * 2^-24 by masking alone (low nibbles; high ones
+    // give 16c * 2^-24), exact, and so are its products with fp16 x in the
+    // fp32 dot2 chains. The offsets (8 per code) are removed afterwards from
+    // the group sum, rescaled by 2^24: the correction is 8 * (sum of the
+    // group's x), computed once per x window. The offset is small next to
+    // the codes, so the chains lose no precision to cancellation. Four
+    // independent dot2 chains.
+    // (Unfolded, for wide batches: the offsets come off each code first,
+    // exactly, in the subnormal range.)
+    __device__ __forceinline__ static float group(const u32x4& w, const u32x4* xv, float corr) {
         constexpr bool fold = M <= kFoldRows;
-        const half2_t off_a = {(half_t)(fold ? 0.0f : -1032.0f), (half_t)(fold ? 0.0f : -1032.0f)};
-        const half2_t off_b = {(half_t)(fold ? 0.0f : -1152.0f), (half_t)(fold ? 0.0f : -1152.0f)};
+        const half2_t off_a = as_half2(0x80088008u);   // -8 * 2^-24, twice
+        const half2_t off_b = as_half2(0x80808080u);   // -128 * 2^-24, twice
         const uint32_t u4[4] = {w.x, w.y, w.z, w.w};
         float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const uint32_t u = u4[d], t = u >> 8;
             const u32x4 xx = xv[d];
-            half2_t ha = as_half2((u & 0x000F000Fu) | vmagic), hb = as_half2((u & 0x00F000F0u) | vmagic);
-            half2_t hc = as_half2((t & 0x000F000Fu) | vmagic), hd = as_half2((t & 0x00F000F0u) | vmagic);
+            half2_t ha = as_half2(u & 0x000F000Fu), hb = as_half2(u & 0x00F000F0u);
+            half2_t hc = as_half2(t & 0x000F000Fu), hd = as_half2(t & 0x00F000F0u);
             if constexpr (!fold) {
                 ha += off_a;
                 hb += off_b;
@@ -373,15 +375,15 @@ struct ChunkMath<M, false> {
             a1 = dot2(hc, as_half2(xx.z), a1);
             b1 = dot2(hd, as_half2(xx.w), b1);
         }
-        const float g = (b0 + b1) * 0.0625f + (a0 + a1);
-        if constexpr (fold) return g - corr;
-        return g;
+        const float g = (b0 + b1) * 0.0625f + (a0 + a1);   // sum of c * x, times 2^-24
+        if constexpr (fold) return fmaf(g, 16777216.0f, -corr);
+        return g * 16777216.0f;
     }
     // xc: the lane's x of block 0 of the chunk; block j is xstep halves on.
     // cc: the lane's correction of block 0; block j is lpr entries on.
     __device__ __forceinline__ static void compute(const u32x4 (&w)[kChunkBlocks], u64 s, const uint16_t* xc,
                                                    const float* cc, int xstride, int cstride, int xstep, int lpr,
-                                                   float (&acc)[M], uint32_t vmagic) {
+                                                   float (&acc)[M]) {
         const uint32_t sw[2] = {(uint32_t)s, (uint32_t)(s >> 32)};
         // blocks in pairs: two groups' math interleaves
 #pragma unroll
@@ -390,8 +392,8 @@ struct ChunkMath<M, false> {
             for (int m = 0; m < M; ++m) {
                 const uint16_t* xm = xc + (size_t)m * xstride + j * xstep;
                 const float* cm = cc + (size_t)m * cstride + j * lpr;
-                const float g0 = group(w[j], reinterpret_cast<const u32x4*>(xm), vmagic, cm[0]);
-                const float g1 = group(w[j + 1], reinterpret_cast<const u32x4*>(xm + xstep), vmagic, cm[lpr]);
+                const float g0 = group(w[j], reinterpret_cast<const u32x4*>(xm), cm[0]);
+                const float g1 = group(w[j + 1], reinterpret_cast<const u32x4*>(xm + xstep), cm[lpr]);
                 acc[m] = fmaf(g0, h2f(uint16_t(sw[j >> 1])), acc[m]);
                 acc[m] = fmaf(g1, h2f(uint16_t(sw[j >> 1] >> 16)), acc[m]);
             }
@@ -423,21 +425,22 @@ struct ChunkMath<M, true> {
                           : u32x4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
         (void)s;
     }
-    // One block (16 codes) against x[16]: bytes q+128 read as fp16
-    // 1024 + (q+128) (one v_perm per pair); the block's correction
-    // (1152 * sum of its x) removes the offset.
+    // One block (16 codes) against x[16]: a byte c = q + 128 becomes the
+    // fp16 subnormal c * 2^-24 (one v_perm per pair, zero high bytes), exact;
+    // the block's correction (128 * sum of its x) removes the offset from the
+    // sum rescaled by 2^24.
     // (Unfolded, for wide batches: the offset comes off each code first.)
     __device__ __forceinline__ static float block(const u32x4& w, const u32x4* xv, float corr) {
         constexpr bool fold = M <= kFoldRows;
-        const half2_t off = {(half_t)-1152.0f, (half_t)-1152.0f};
+        const half2_t off = as_half2(0x80808080u);   // -128 * 2^-24, twice
         const uint32_t u4[4] = {w.x, w.y, w.z, w.w};
         const u32x4 x0 = xv[0], x1 = xv[1];
         const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-            half2_t lo = as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04010400u));
-            half2_t hi = as_half2(__builtin_amdgcn_perm(0x64646464u, u4[d], 0x04030402u));
+            half2_t lo = as_half2(__builtin_amdgcn_perm(0u, u4[d], 0x0c010c00u));
+            half2_t hi = as_half2(__builtin_amdgcn_perm(0u, u4[d], 0x0c030c02u));
             if constexpr (!fold) {
                 lo += off;
                 hi += off;
@@ -445,12 +448,12 @@ struct ChunkMath<M, true> {
             a0 = dot2(lo, as_half2(xw[2 * d]), a0);
             a1 = dot2(hi, as_half2(xw[2 * d + 1]), a1);
         }
-        if constexpr (fold) return (a0 + a1) - corr;
-        return a0 + a1;
+        if constexpr (fold) return fmaf(a0 + a1, 16777216.0f, -corr);
+        return (a0 + a1) * 16777216.0f;
     }
     __device__ __forceinline__ static void compute(const u32x4 (&w)[kChunkBlocks], u64, const uint16_t* xc,
                                                    const float* cc, int xstride, int cstride, int xstep, int lpr,
-                                                   float (&acc)[M], uint32_t) {
+                                                   float (&acc)[M]) {
 #pragma unroll
         for (int j = 0; j < kChunkBlocks; j += 2) {
 #pragma unroll
@@ -789,29 +792,16 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     }
 
     // ---- offset corrections of the window's units (after the x window):
-    // int4 group 1032 * (x at k%8 in {0,1,4,5}) + 72 * (x at k%8 in {2,3,6,7});
-    // int8 block 1152 * sum of its 16 x
+    // int4 group 8 * (sum of its 32 x); int8 block 128 * (sum of its 16 x)
     const int xstride = p.win * CK;
     const int cstride = xstride / CM::kUnit;
     float* corr = reinterpret_cast<float*>(smem + ((size_t)M * xstride * 2 + 15) / 16 * 16);
     for (int i = tid; i < (M <= kFoldRows ? M * cstride : 0); i += kThreads) {
         const uint16_t* xu = xs + (size_t)i * CM::kUnit;   // rows are contiguous: unit i of the window
-        float c;
-        if constexpr (Q8) {
-            float s16 = 0.0f;
+        float sum = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s16 += h2f(xu[e]);
-            c = 1152.0f * s16;
-        } else {
-            float sa = 0.0f, sb = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 32; ++e) {
-                if ((e & 2) == 0) sa += h2f(xu[e]);
-                else sb += h2f(xu[e]);
-            }
-            c = 1032.0f * sa + 72.0f * sb;
-        }
-        corr[i] = c;
+        for (int e = 0; e < CM::kUnit; ++e) sum += h2f(xu[e]);
+        corr[i] = (Q8 ? 128.0f : 8.0f) * sum;
     }
     if constexpr (M <= kFoldRows) __syncthreads();
 
@@ -824,9 +814,6 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     for (int q = 0; q < kPieces; ++q)
 #pragma unroll
         for (int m = 0; m < M; ++m) accq[q][m] = 0.0f;
-
-    uint32_t vmagic;
-    asm("v_mov_b32 %0, %1" : "=v"(vmagic) : "s"(0x64006400u));
 
     if (w0 < w1) {
         int f = w0;
@@ -845,8 +832,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         // the tile ends.
         auto step = [&](u32x4 (&wbuf)[kChunkBlocks], u64& sbuf, bool refill) -> bool {
             CM::compute(wbuf, sbuf, xs + (size_t)(c - p.ca) * CK + xsub,
-                        corr + (size_t)(c - p.ca) * (CK / CM::kUnit) + usub, xstride, cstride, xstep, A.lpr, acc,
-                        vmagic);
+                        corr + (size_t)(c - p.ca) * (CK / CM::kUnit) + usub, xstride, cstride, xstep, A.lpr, acc);
             const bool end = f + 1 == w1;
             if (c + 1 == cend || c + 1 == A.chunks || end) {
 #pragma unroll
@@ -1883,10 +1869,13 @@ int launch(const StepArgs* d_args, int grid, size_t lds, hipStream_t st) {
             return LYK_ERR_SHAPE;
         fits_lds = lds;
     }
-    void* params[] = {&d_args};
-    if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(grid), dim3(kThreads), params,
-                                   (unsigned)lds, st) != hipSuccess)
-        return LYK_ERR_LAUNCH;
+    // A plain launch: with more than half of a CU's LDS per workgroup the
+    // grid (one workgroup per CU) is resident at once on an otherwise idle
+    // device, which the occupancy check above guarantees the kernel can
+    // reach; were a workgroup ever held back, the waits it blocks are
+    // bounded and end the launch with the workspace error word set.
+    kern<<<dim3(grid), dim3(kThreads), lds, st>>>(d_args);
+    if (hipGetLastError() != hipSuccess) return LYK_ERR_LAUNCH;
     return LYK_OK;
 }
 
@@ -1909,16 +1898,28 @@ int launch_hd(int hd, int m, const StepArgs* d_args, int grid, size_t lds, hipSt
     }
 }
 
-// Launch arguments live in the workspace; they are uploaded (in stream
-// order) only when they differ from the last ones written to that
-// workspace, so a run of identical steps (GreedyRun) uploads once.
-struct ArgsCache {
-    std::mutex mu;
-    std::unordered_map<const void*, StepArgs> last;
+// Launches one workspace serves before it is zeroed again. Tags are
+// (launches completed + 1) << 8 | layer in 32 bits, so they stay nonzero and
+// distinct for 2^24 - 1 launches; the host re-zeroes the workspace (every
+// tagged word and counter) first when the next launch would reach that.
+constexpr uint64_t kTagEpochLaunches = (1ull << 24) - 1;
+
+// Host-side state per workspace: the launch arguments last uploaded (they
+// live in the workspace and are re-uploaded, in stream order, only when
+// they change, so a run of identical steps uploads once) and the launches
+// queued since the workspace was last zeroed.
+struct WorkspaceState {
+    StepArgs last;
+    bool has_last = false;
+    uint64_t launches = 0;
 };
-ArgsCache& args_cache() {
-    static ArgsCache c;
-    return c;
+struct WorkspaceTable {
+    std::mutex mu;
+    std::unordered_map<const void*, WorkspaceState> by_ws;
+};
+WorkspaceTable& workspaces() {
+    static WorkspaceTable* t = new WorkspaceTable;   // never destroyed: no teardown-order dependence at exit
+    return *t;
 }
 
 }  // namespace
@@ -1992,34 +1993,71 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     a.attn_split_tokens = model->attn_split_tokens ? model->attn_split_tokens : kAttnSplitTokens;
     a.attn_max_splits = model->attn_max_splits ? model->attn_max_splits : kAttnDefaultSplits;
     a.phases = (int)lyk_hip_step_phases(model, io->mode);
+    a.spin_ticks = model->wait_limit_us ? (uint64_t)model->wait_limit_us * 100u : kSpinTicks;
     const Staging sg = gateup_staging(*model, m, grid);
     a.pf_off = sg.off;
     a.pf_chunks = sg.chunks;
     hipStream_t st = static_cast<hipStream_t>(stream);
     StepArgs* d_args = reinterpret_cast<StepArgs*>(ws + L.args);
-    {
-        ArgsCache& cache = args_cache();
-        std::lock_guard<std::mutex> lock(cache.mu);
-        auto it = cache.last.find(d_workspace);
-        if (it == cache.last.end() || std::memcmp(&it->second, &a, sizeof a) != 0) {
-            if (hipMemcpyAsync(d_args, &a, sizeof a, hipMemcpyHostToDevice, st) != hipSuccess) return LYK_ERR_HIP;
-            cache.last[d_workspace] = a;
-        }
+    WorkspaceTable& tab = workspaces();
+    std::lock_guard<std::mutex> lock(tab.mu);
+    WorkspaceState& w = tab.by_ws[d_workspace];
+    if (w.launches >= kTagEpochLaunches) {
+        // a new tag epoch: no word from before can match a tag again
+        if (hipMemsetAsync(d_workspace, 0, workspace_bytes, st) != hipSuccess) return LYK_ERR_HIP;
+        w.launches = 0;
+        w.has_last = false;
+    }
+    if (!w.has_last || std::memcmp(&w.last, &a, sizeof a) != 0) {
+        if (hipMemcpyAsync(d_args, &a, sizeof a, hipMemcpyHostToDevice, st) != hipSuccess) return LYK_ERR_HIP;
+        w.last = a;
+        w.has_last = true;
     }
     rc = model->q8 ? launch_hd<true>(model->head_dim, m, d_args, grid, lds, st)
                    : launch_hd<false>(model->head_dim, m, d_args, grid, lds, st);
+    if (rc == LYK_OK) ++w.launches;
     return rc;
 }
 
 int lyk_hip_step_reset(void* d_workspace, uint64_t workspace_bytes, void* stream) {
     if (!d_workspace) return LYK_ERR_INVALID_ARG;
-    {
-        ArgsCache& cache = args_cache();
-        std::lock_guard<std::mutex> lock(cache.mu);
-        cache.last.erase(d_workspace);
-    }
+    WorkspaceTable& tab = workspaces();
+    std::lock_guard<std::mutex> lock(tab.mu);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (hipMemsetAsync(d_workspace, 0, workspace_bytes, st) != hipSuccess) return LYK_ERR_HIP;
+    tab.by_ws[d_workspace] = WorkspaceState{};
+    return LYK_OK;
+}
+
+uint64_t lyk_hip_step_launches(const void* d_workspace) {
+    WorkspaceTable& tab = workspaces();
+    std::lock_guard<std::mutex> lock(tab.mu);
+    const auto it = tab.by_ws.find(d_workspace);
+    return it == tab.by_ws.end() ? 0 : it->second.launches;
+}
+
+int lyk_hip_step_set_launches(const lyk_step_model* model, int max_rows, void* d_workspace,
+                              uint64_t workspace_bytes, uint64_t launches, void* stream) {
+    if (!model || !d_workspace || max_rows < 1 || max_rows > kMaxRows || launches > kTagEpochLaunches)
+        return LYK_ERR_INVALID_ARG;
+    if (check_model(*model) != LYK_OK) return LYK_ERR_INVALID_ARG;
+    const int grid = step_grid();
+    if (grid < 1) return LYK_ERR_HIP;
+    const Layout L = layout(*model, max_rows, grid);
+    if (L.total > workspace_bytes) return LYK_ERR_WORKSPACE;
+    WorkspaceTable& tab = workspaces();
+    std::lock_guard<std::mutex> lock(tab.mu);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (hipMemsetAsync(d_workspace, 0, workspace_bytes, st) != hipSuccess) return LYK_ERR_HIP;
+    // every workgroup's counter; the host copy is synchronous (pageable
+    // source), so the vector may go out of scope afterwards
+    std::vector<uint32_t> seq((size_t)grid, (uint32_t)launches);
+    if (hipStreamSynchronize(st) != hipSuccess ||
+        hipMemcpy(static_cast<char*>(d_workspace) + L.seq, seq.data(), seq.size() * 4, hipMemcpyHostToDevice) !=
+            hipSuccess)
+        return LYK_ERR_HIP;
+    tab.by_ws[d_workspace] = WorkspaceState{};
+    tab.by_ws[d_workspace].launches = launches;
     return LYK_OK;
 }
 

@@ -76,6 +76,8 @@ _KERNEL_SIGS = {
     "lyk_hip_decode_step": (I, [P, P, P, U64, I, P]),
     "lyk_hip_step_reset": (I, [P, U64, P]),
     "lyk_hip_step_error": (I, [P, C.POINTER(C.c_int32), P]),
+    "lyk_hip_step_launches": (U64, [P]),
+    "lyk_hip_step_set_launches": (I, [P, I, P, U64, U64, P]),
 }
 
 class ModelConfig(C.Structure):
@@ -98,6 +100,7 @@ _MODEL_SIGS = {
     "lyk_model_load_safetensors": (P, [C.c_char_p, C.POINTER(ModelConfig), C.POINTER(ModelOptions), I32P]),
     "lyk_model_load_synthetic": (P, [C.POINTER(ModelConfig), U64, F, C.POINTER(ModelOptions), I32P]),
     "lyk_model_free": (None, [P]),
+    "lyk_model_read_tensor_f32": (C.c_int32, [C.c_char_p, C.c_char_p, P, U64, C.POINTER(U64)]),
     "lyk_model_seq_new": (P, [P, U32, C.c_int32, C.c_char_p, I32P]),
     "lyk_model_seq_free": (None, [P]),
     "lyk_model_seq_length": (U32, [P]),
@@ -113,6 +116,9 @@ _MODEL_SIGS = {
     "lyk_model_set_step_tracing": (C.c_int32, [P, C.c_int32]),
     "lyk_model_stream": (P, [P]),
     "lyk_model_step_trace": (C.c_size_t, [P, P, C.c_size_t]),
+    "lyk_model_step_launches": (U64, [P]),
+    "lyk_model_set_wait_limit": (None, [P, U32]),
+    "lyk_model_set_step_launches": (C.c_int32, [P, U64]),
     "lyk_synth_normal": (None, [U64, U64, U64, U64, F, P]),
 }
 

@@ -169,6 +169,20 @@ class HipModel:
         """hipStream_t of the model (for torch.cuda.ExternalStream)."""
         return L.model_lib().lyk_model_stream(self._h)
 
+    @property
+    def step_launches(self):
+        """Fused-step launches since the step workspace was last zeroed."""
+        return L.model_lib().lyk_model_step_launches(self._h)
+
+    def set_step_launches(self, n):
+        """Zeroes the step workspace and presets its launch count (tests of
+        the 2^24 - 1 launch-tag limit)."""
+        L.check("lyk_model_set_step_launches", L.model_lib().lyk_model_set_step_launches(self._h, n))
+
+    def set_wait_limit(self, microseconds):
+        """Bound of the fused step's waits for other workgroups (0: 2 s)."""
+        L.model_lib().lyk_model_set_wait_limit(self._h, microseconds)
+
     def set_step_tracing(self, on=True):
         L.check("lyk_model_set_step_tracing", L.model_lib().lyk_model_set_step_tracing(self._h, int(on)))
 
@@ -205,6 +219,17 @@ class Sequence:
     @property
     def capacity(self):
         return L.model_lib().lyk_model_seq_capacity(self._h)
+
+
+def read_tensor_f32(path, name):
+    """(status, fp32 array) of one tensor as the loader reads it (no GPU)."""
+    n = C.c_uint64(0)
+    code = L.model_lib().lyk_model_read_tensor_f32(path.encode(), name.encode(), None, 0, C.byref(n))
+    if code != OK:
+        return code, None
+    out = np.empty(n.value, np.float32)
+    code = L.model_lib().lyk_model_read_tensor_f32(path.encode(), name.encode(), _p(out), n.value, C.byref(n))
+    return code, out
 
 
 def synth_normal(seed, stream, count, sigma, first=0):

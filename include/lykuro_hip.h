@@ -321,6 +321,10 @@ typedef struct lyk_step_model {
     /* Gate/up chunks per wave staged in LDS while the attention and O phases
      * run: 0 = as many as fit, -1 = none, n > 0 = at most n. */
     int32_t lds_prefetch;
+    /* A step's waits for other workgroups' words give up after this many
+     * microseconds (0: 2 s); the step then ends with the workspace error
+     * word set. Small values force that failure path in tests. */
+    uint32_t wait_limit_us;
     const float* embed;      /* fp32 [vocab][hidden] */
     const float* final_norm;
     const void* lm_head_w;
@@ -381,6 +385,19 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io,
                         void* stream);
 /* Zeroes the workspace (stream-ordered) and forgets its cached arguments. */
 int lyk_hip_step_reset(void* d_workspace, uint64_t workspace_bytes, void* stream);
+/* Launch tags. Every word one workgroup hands another carries the tag
+ * (launches completed + 1) << 8 | layer, 32 bits: distinct and nonzero for
+ * 2^24 - 1 launches of one workspace. lyk_hip_decode_step counts the launches
+ * it queues on each workspace and zeroes the workspace (stream-ordered) before
+ * the launch that would reach that count, so a long-running host never sees
+ * a tag repeat. lyk_hip_step_launches returns the count since the last
+ * zeroing; lyk_hip_step_set_launches zeroes the workspace and sets every
+ * workgroup's counter and the host count to `launches` (<= 2^24 - 1) -- for
+ * tests that cross the limit without running 2^24 steps. No counterpart in
+ * the reference (its CUDA backend has no cross-workgroup dataflow). */
+uint64_t lyk_hip_step_launches(const void* d_workspace);
+int lyk_hip_step_set_launches(const lyk_step_model* model, int max_rows, void* d_workspace,
+                              uint64_t workspace_bytes, uint64_t launches, void* stream);
 /* Copies the error word (0 = no error) to *error_out and waits for it. */
 int lyk_hip_step_error(const void* d_workspace, int32_t* error_out, void* stream);
 int lyk_abi_version(void);

@@ -57,6 +57,15 @@ void* lyk_model_load_safetensors(const char* path, const lyk_model_config* confi
 void* lyk_model_load_synthetic(const lyk_model_config* config, uint64_t seed, float sigma,
                                const lyk_model_options* options, int32_t* status);
 void lyk_model_free(void* model);
+/* The loader's view of one tensor, without a device: opens the file with the
+ * reader's checks (model/loader/safetensors.cpp:160-297: regular file, no
+ * symlink, header bounds, dtype allow-list, rank <= 8, offsets tiling the
+ * data) and widens F16/BF16 to fp32 as the loader does
+ * (backends/cpu/cpu_backend.cpp:8-50). Writes min(max_count, elements)
+ * floats to out and the element count to *count; returns the ErrorCode
+ * value. */
+int32_t lyk_model_read_tensor_f32(const char* path, const char* name, float* out, uint64_t max_count,
+                                  uint64_t* count);
 
 /* CreateSequence / CreateSequenceEx (generative_model.h:47-56). */
 void* lyk_model_seq_new(void* model, uint32_t max_tokens, int32_t allow_prefix_cache,
@@ -92,6 +101,18 @@ int32_t lyk_model_set_step_tracing(void* model, int32_t on);
  * for callers that time it with events. */
 void* lyk_model_stream(void* model);
 size_t lyk_model_step_trace(void* model, uint64_t* out, size_t max);
+/* Launch-tag epoch of the model's fused step (lyk_hip_step_launches /
+ * lyk_hip_step_set_launches): launches since the workspace was last zeroed,
+ * and a preset of that count for tests that cross the 2^24 - 1 limit. No
+ * counterpart in the reference. */
+uint64_t lyk_model_step_launches(const void* model);
+/* Limit of the fused step's waits for other workgroups, in microseconds
+ * (0: 2 s, the default). A step that exceeds it ends unfinished: the call
+ * returns gpu_unhealthy (14), no sequence advances, and the next call runs
+ * on a reset workspace. Small values exercise that path in tests. No
+ * counterpart in the reference. */
+void lyk_model_set_wait_limit(void* model, uint32_t microseconds);
+int32_t lyk_model_set_step_launches(void* model, uint64_t launches);
 
 /* Seeded N(0, sigma^2) stream: value i of stream `stream` depends only on
  * (seed, stream, i); Box-Muller on splitmix64 outputs. */

@@ -111,12 +111,14 @@ def lib():
             "orc_rmsnorm": (None, [P, P, C.c_float, i64, P]),
             "orc_rope": (None, [P, u32, u32, C.c_float]),
             "orc_attention": (None, [P, P, P, u32, u32, u32, u32, P]),
+            "orc_attention_mt": (None, [P, P, P, u32, u32, u32, u32, P, C.c_int]),
             "orc_model_new": (P, [C.POINTER(_Config)]),
             "orc_model_free": (None, [P]),
             "orc_model_tensor": (C.POINTER(C.c_float), [P, C.c_int, u32]),
             "orc_model_tensor_numel": (u64, [P, C.c_int]),
             "orc_model_set_threads": (None, [P, C.c_int]),
             "orc_model_set_f16_mirror": (None, [P, C.c_int]),
+            "orc_model_set_descending_sums": (None, [P, C.c_int]),
             "orc_seq_new": (P, [P, u32]), "orc_seq_free": (None, [P]),
             "orc_seq_length": (u32, [P]),
             "orc_prefill": (C.c_int, [P, P, P, C.c_size_t, P]),
@@ -190,21 +192,34 @@ def round_f16(x):
 
 
 # ------------------------------------------------------------ quantizers
+def _by_rows(n, k, call):
+    """call(a, b) over row blocks [a, b) in parallel; the quantizers work row
+    by row, so the result equals one call over all rows."""
+    futs = [_pool().submit(call, a, b) for a, b in _split(n, max(1, (1 << 20) // max(1, k))) if b > a]
+    for f in futs:
+        f.result()
+
+
+def _rp(x, a):
+    """Pointer to row a of x."""
+    return C.c_void_p(x.ctypes.data + a * x.strides[0])
+
+
 def q4_quantize(w):
     """int4 g32 fp16-scale codes [N,K] int8 and scales [N,ceil(K/32)] fp16 bits."""
     w = np.ascontiguousarray(w, dtype=np.float32)
     n, k = w.shape
     codes = np.empty((n, k), np.int8)
     scales = np.empty((n, (k + 31) // 32), np.uint16)
-    lib().orc_q4_quantize(_p(w), n, k, _p(codes), _p(scales))
+    _by_rows(n, k, lambda a, b: lib().orc_q4_quantize(_rp(w, a), b - a, k, _rp(codes, a), _rp(scales, a)))
     return codes, scales
 
 
 def q4_dequantize(codes, scales):
     n, k = codes.shape
     out = np.empty((n, k), np.float32)
-    lib().orc_q4_dequantize(_p(np.ascontiguousarray(codes)), _p(np.ascontiguousarray(scales)),
-                            n, k, _p(out))
+    codes, scales = np.ascontiguousarray(codes), np.ascontiguousarray(scales)
+    _by_rows(n, k, lambda a, b: lib().orc_q4_dequantize(_rp(codes, a), _rp(scales, a), b - a, k, _rp(out, a)))
     return out
 
 
@@ -213,15 +228,15 @@ def q8_quantize(w):
     n, k = w.shape
     codes = np.empty((n, k), np.int8)
     scales = np.empty((n,), np.uint16)
-    lib().orc_q8_quantize(_p(w), n, k, _p(codes), _p(scales))
+    _by_rows(n, k, lambda a, b: lib().orc_q8_quantize(_rp(w, a), b - a, k, _rp(codes, a), _rp(scales, a)))
     return codes, scales
 
 
 def q8_dequantize(codes, scales):
     n, k = codes.shape
     out = np.empty((n, k), np.float32)
-    lib().orc_q8_dequantize(_p(np.ascontiguousarray(codes)), _p(np.ascontiguousarray(scales)),
-                            n, k, _p(out))
+    codes, scales = np.ascontiguousarray(codes), np.ascontiguousarray(scales)
+    _by_rows(n, k, lambda a, b: lib().orc_q8_dequantize(_rp(codes, a), _rp(scales, a), b - a, k, _rp(out, a)))
     return out
 
 
@@ -258,19 +273,47 @@ def rope(vec, pos, theta):
     return v
 
 
-def attention(q, keys, values, heads, kv_heads, head_dim):
+def attention(q, keys, values, heads, kv_heads, head_dim, threads=1):
     q = np.ascontiguousarray(q, dtype=np.float32)
     keys = np.ascontiguousarray(keys, dtype=np.float32)
     values = np.ascontiguousarray(values, dtype=np.float32)
     out = np.empty(heads * head_dim, np.float32)
-    lib().orc_attention(_p(q), _p(keys), _p(values), keys.shape[0], heads, kv_heads,
-                        head_dim, _p(out))
+    if threads > 1:
+        lib().orc_attention_mt(_p(q), _p(keys), _p(values), keys.shape[0], heads, kv_heads,
+                               head_dim, _p(out), threads)
+    else:
+        lib().orc_attention(_p(q), _p(keys), _p(values), keys.shape[0], heads, kv_heads,
+                            head_dim, _p(out))
     return out
 
 
+_POOL = None
+
+
+def _pool():
+    """Worker threads for the row- or element-independent helpers below
+    (ctypes releases the GIL around each C call)."""
+    global _POOL
+    if _POOL is None:
+        from concurrent.futures import ThreadPoolExecutor
+        _POOL = ThreadPoolExecutor(max(1, min(16, os.cpu_count() or 1)))
+    return _POOL
+
+
+def _split(total, min_piece):
+    n = max(1, min(_pool()._max_workers, total // max(1, min_piece)))
+    return [(total * i // n, total * (i + 1) // n) for i in range(n)]
+
+
 def synth_normal(seed, stream, count, sigma, first=0):
+    """Value i depends only on (seed, stream, first + i): chunks computed in
+    parallel equal the serial stream."""
     out = np.empty(count, np.float32)
-    lib().orc_synth_normal(seed, stream, first, count, sigma, _p(out))
+    parts = _split(count, 1 << 20)
+    futs = [_pool().submit(lib().orc_synth_normal, seed, stream, first + a, b - a, sigma,
+                           out[a:b].ctypes.data_as(C.c_void_p)) for a, b in parts if b > a]
+    for f in futs:
+        f.result()
     return out
 
 
@@ -296,8 +339,8 @@ class OracleModel:
         lib().orc_model_set_threads(self._h, threads)
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            lib().orc_model_free(self._h)
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.orc_model_free(self._h)
             self._h = None
 
     def tensor(self, kind, layer=0):
@@ -326,6 +369,9 @@ class OracleModel:
     def set_f16_mirror(self, on):
         lib().orc_model_set_f16_mirror(self._h, int(on))
 
+    def set_descending_sums(self, on):
+        lib().orc_model_set_descending_sums(self._h, int(on))
+
     def new_seq(self, max_tokens):
         return _Seq(self, max_tokens)
 
@@ -347,8 +393,8 @@ class _Seq:
         self._h = lib().orc_seq_new(model._h, max_tokens)
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            lib().orc_seq_free(self._h)
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.orc_seq_free(self._h)
             self._h = None
 
     @property

@@ -172,23 +172,46 @@ void orc_matvec(const float* w, const float* bias, const float* x,
     }
 }
 
+/* The same sum with the products added in descending index order: a second,
+ * equally valid fp32 order (not the reference's), for measuring how much a
+ * result depends on summation order alone. */
+static void matvec_descending(const float* w, const float* bias, const float* x,
+                              int64_t in_dim, int64_t out_dim, float* out) {
+    for (int64_t o = 0; o < out_dim; ++o) {
+        const float* row = w + o * in_dim;
+        float acc = bias ? bias[o] : 0.0f;
+        for (int64_t i = in_dim; i-- > 0;) acc += row[i] * x[i];
+        out[o] = acc;
+    }
+}
+
 typedef struct {
     const float *w, *bias, *x;
     int64_t in_dim, r0, r1;
     float* out;
+    int descending;
 } mv_job;
 
 static void* mv_worker(void* p) {
     mv_job* j = (mv_job*)p;
-    orc_matvec(j->w + j->r0 * j->in_dim, j->bias ? j->bias + j->r0 : NULL, j->x,
-               j->in_dim, j->r1 - j->r0, j->out + j->r0);
+    (j->descending ? matvec_descending : orc_matvec)(j->w + j->r0 * j->in_dim,
+                                                     j->bias ? j->bias + j->r0 : NULL, j->x,
+                                                     j->in_dim, j->r1 - j->r0, j->out + j->r0);
     return NULL;
 }
 
+static void matvec_rows(const float* w, const float* bias, const float* x, int64_t in_dim,
+                        int64_t out_dim, float* out, int threads, int descending);
+
 void orc_matvec_mt(const float* w, const float* bias, const float* x,
                    int64_t in_dim, int64_t out_dim, float* out, int threads) {
+    matvec_rows(w, bias, x, in_dim, out_dim, out, threads, 0);
+}
+
+static void matvec_rows(const float* w, const float* bias, const float* x, int64_t in_dim,
+                        int64_t out_dim, float* out, int threads, int descending) {
     if (threads <= 1 || out_dim * in_dim < (1 << 18)) {
-        orc_matvec(w, bias, x, in_dim, out_dim, out);
+        (descending ? matvec_descending : orc_matvec)(w, bias, x, in_dim, out_dim, out);
         return;
     }
     if (threads > 64) threads = 64;
@@ -200,6 +223,7 @@ void orc_matvec_mt(const float* w, const float* bias, const float* x,
         jobs[t].in_dim = in_dim; jobs[t].out = out;
         jobs[t].r0 = out_dim * t / threads;
         jobs[t].r1 = out_dim * (t + 1) / threads;
+        jobs[t].descending = descending;
     }
     for (int t = 1; t < threads; ++t)
         spawned[t] = pthread_create(&tid[t], NULL, mv_worker, &jobs[t]) == 0;
@@ -232,15 +256,16 @@ void orc_rope(float* vec, uint32_t head_dim, uint32_t pos, float theta) {
     }
 }
 
-void orc_attention(const float* q, const float* keys, const float* values,
-                   uint32_t context, uint32_t heads, uint32_t kv_heads,
-                   uint32_t head_dim, float* out) {
+/* Query heads [h0, h1) of orc_attention. */
+static void attention_heads(const float* q, const float* keys, const float* values,
+                            uint32_t context, uint32_t heads, uint32_t kv_heads,
+                            uint32_t head_dim, uint32_t h0, uint32_t h1, float* out) {
     /* qwen_model.cpp:255-287 */
     const uint32_t group = heads / kv_heads;
     const size_t stride = (size_t)kv_heads * head_dim;
     const float scale = 1.0f / sqrtf((float)head_dim);
     float* scores = (float*)malloc(sizeof(float) * (context ? context : 1));
-    for (uint32_t h = 0; h < heads; ++h) {
+    for (uint32_t h = h0; h < h1; ++h) {
         const uint32_t kvh = h / group;
         const float* qh = q + (size_t)h * head_dim;
         float mx = -INFINITY;
@@ -267,6 +292,53 @@ void orc_attention(const float* q, const float* keys, const float* values,
     free(scores);
 }
 
+void orc_attention(const float* q, const float* keys, const float* values,
+                   uint32_t context, uint32_t heads, uint32_t kv_heads,
+                   uint32_t head_dim, float* out) {
+    attention_heads(q, keys, values, context, heads, kv_heads, head_dim, 0, heads, out);
+}
+
+typedef struct {
+    const float *q, *keys, *values;
+    uint32_t context, heads, kv_heads, head_dim, h0, h1;
+    float* out;
+} att_job;
+
+static void* att_worker(void* p) {
+    const att_job* j = (const att_job*)p;
+    attention_heads(j->q, j->keys, j->values, j->context, j->heads, j->kv_heads,
+                    j->head_dim, j->h0, j->h1, j->out);
+    return NULL;
+}
+
+void orc_attention_mt(const float* q, const float* keys, const float* values,
+                      uint32_t context, uint32_t heads, uint32_t kv_heads,
+                      uint32_t head_dim, float* out, int threads) {
+    /* each head is computed by the same code whatever thread runs it */
+    if (threads > (int)heads) threads = (int)heads;
+    if (threads > 64) threads = 64;
+    if (threads <= 1 || (uint64_t)context * heads * head_dim < (1u << 18)) {
+        orc_attention(q, keys, values, context, heads, kv_heads, head_dim, out);
+        return;
+    }
+    pthread_t tid[64];
+    int spawned[64] = {0};
+    att_job jobs[64];
+    for (int t = 0; t < threads; ++t) {
+        att_job j = {q, keys, values, context, heads, kv_heads, head_dim,
+                     (uint32_t)((uint64_t)heads * t / threads),
+                     (uint32_t)((uint64_t)heads * (t + 1) / threads), out};
+        jobs[t] = j;
+    }
+    for (int t = 1; t < threads; ++t)
+        spawned[t] = pthread_create(&tid[t], NULL, att_worker, &jobs[t]) == 0;
+    att_worker(&jobs[0]);
+    for (int t = 1; t < threads; ++t) {
+        if (spawned[t]) pthread_join(tid[t], NULL);
+        else att_worker(&jobs[t]);
+    }
+}
+
 /* ------------------------------------------------------------------- model */
 
 struct orc_model {
@@ -275,6 +347,7 @@ struct orc_model {
     float** layer_t[ORC_T_COUNT];     /* per-layer tensors */
     int threads;
     int f16_mirror;
+    int descending;   /* forward matvecs add products in descending index order */
 };
 
 struct orc_seq {
@@ -357,6 +430,8 @@ void orc_model_set_threads(orc_model* m, int threads) {
 
 void orc_model_set_f16_mirror(orc_model* m, int on) { m->f16_mirror = on; }
 
+void orc_model_set_descending_sums(orc_model* m, int on) { m->descending = on; }
+
 orc_seq* orc_seq_new(const orc_model* m, uint32_t max_tokens) {
     orc_seq* s = (orc_seq*)calloc(1, sizeof(orc_seq));
     s->max_tokens = max_tokens;
@@ -409,34 +484,34 @@ static void forward_token(const orc_model* m, orc_seq* s, uint32_t token,
 #define LT(kind) (m->layer_t[kind][l])
         orc_rmsnorm(hidden, LT(ORC_T_INPUT_NORM), c->rms_norm_eps, h, normed);
         mirror_round(m, normed, h);
-        orc_matvec_mt(LT(ORC_T_Q_W), LT(ORC_T_Q_B), normed, h, qd, q, T);
+        matvec_rows(LT(ORC_T_Q_W), LT(ORC_T_Q_B), normed, h, qd, q, T, m->descending);
         float* k = s->keys[l] + (size_t)pos * kvd;
         float* v = s->values[l] + (size_t)pos * kvd;
-        orc_matvec_mt(LT(ORC_T_K_W), LT(ORC_T_K_B), normed, h, kvd, k, T);
-        orc_matvec_mt(LT(ORC_T_V_W), LT(ORC_T_V_B), normed, h, kvd, v, T);
+        matvec_rows(LT(ORC_T_K_W), LT(ORC_T_K_B), normed, h, kvd, k, T, m->descending);
+        matvec_rows(LT(ORC_T_V_W), LT(ORC_T_V_B), normed, h, kvd, v, T, m->descending);
         for (uint32_t hh = 0; hh < c->num_heads; ++hh)
             orc_rope(q + (size_t)hh * c->head_dim, c->head_dim, pos, c->rope_theta);
         for (uint32_t hh = 0; hh < c->num_kv_heads; ++hh)
             orc_rope(k + (size_t)hh * c->head_dim, c->head_dim, pos, c->rope_theta);
         mirror_round(m, k, kvd);
         mirror_round(m, v, kvd);
-        orc_attention(q, s->keys[l], s->values[l], pos + 1, c->num_heads,
-                      c->num_kv_heads, c->head_dim, attn);
+        orc_attention_mt(q, s->keys[l], s->values[l], pos + 1, c->num_heads,
+                         c->num_kv_heads, c->head_dim, attn, T);
         mirror_round(m, attn, qd);
-        orc_matvec_mt(LT(ORC_T_O_W), NULL, attn, qd, h, proj, T);
+        matvec_rows(LT(ORC_T_O_W), NULL, attn, qd, h, proj, T, m->descending);
         for (size_t i = 0; i < h; ++i) hidden[i] += proj[i];
 
         orc_rmsnorm(hidden, LT(ORC_T_POST_NORM), c->rms_norm_eps, h, normed);
         mirror_round(m, normed, h);
-        orc_matvec_mt(LT(ORC_T_GATE_W), NULL, normed, h, I, gate, T);
-        orc_matvec_mt(LT(ORC_T_UP_W), NULL, normed, h, I, up, T);
+        matvec_rows(LT(ORC_T_GATE_W), NULL, normed, h, I, gate, T, m->descending);
+        matvec_rows(LT(ORC_T_UP_W), NULL, normed, h, I, up, T, m->descending);
         for (size_t i = 0; i < I; ++i) {
             const float x = gate[i];
             const float silu = x / (1.0f + expf(-x));
             gate[i] = silu * up[i];
         }
         mirror_round(m, gate, I);
-        orc_matvec_mt(LT(ORC_T_DOWN_W), NULL, gate, I, h, proj, T);
+        matvec_rows(LT(ORC_T_DOWN_W), NULL, gate, I, h, proj, T, m->descending);
         for (size_t i = 0; i < h; ++i) hidden[i] += proj[i];
 #undef LT
     }
@@ -453,8 +528,8 @@ static int logits_from_hidden(const orc_model* m, const float* hidden,
     mirror_round(m, normed, c->hidden_size);
     const float* head = c->tie_word_embeddings ? m->model_t[ORC_T_EMBED]
                                                : m->model_t[ORC_T_LM_HEAD];
-    orc_matvec_mt(head, NULL, normed, c->hidden_size, c->vocab_size, logits,
-                  m->threads);
+    matvec_rows(head, NULL, normed, c->hidden_size, c->vocab_size, logits,
+                m->threads, m->descending);
     free(normed);
     for (uint32_t i = 0; i < c->vocab_size; ++i)
         if (!isfinite(logits[i])) return ORC_INFERENCE_FAILED;

@@ -96,6 +96,10 @@ void orc_rope(float* vec, uint32_t head_dim, uint32_t pos, float theta);
 void orc_attention(const float* q, const float* keys, const float* values,
                    uint32_t context, uint32_t heads, uint32_t kv_heads,
                    uint32_t head_dim, float* out);
+/* Same, query heads split over `threads` threads: bit-identical. */
+void orc_attention_mt(const float* q, const float* keys, const float* values,
+                      uint32_t context, uint32_t heads, uint32_t kv_heads,
+                      uint32_t head_dim, float* out, int threads);
 
 /* ---- model (qwen_model.cpp:88-412) ---- */
 typedef struct orc_config {
@@ -135,11 +139,25 @@ void orc_model_free(orc_model* m);
  * for model-level tensors. */
 float* orc_model_tensor(orc_model* m, int kind, uint32_t layer);
 uint64_t orc_model_tensor_numel(const orc_model* m, int kind);
-/* Worker threads for the matvecs (results are identical for any count). */
+/* Worker threads for the matvecs and attention heads (results are identical
+ * for any count). */
 void orc_model_set_threads(orc_model* m, int threads);
-/* Diagnostic mode, not the reference: round every matvec input and every
- * stored K/V row to fp16, the storage points of the HIP decode path. */
+/* fp16 mirror mode, a test bar rather than the reference: the forward above
+ * with five values rounded to fp16 (RNE, orc_f32_to_f16) where the HIP decode
+ * path stores them in fp16 -- the RMSNorm output feeding each matvec (QKV,
+ * gate/up, LM head), the RoPE-rotated key and the value written to the cache,
+ * the attention output feeding o_proj, and SiLU(gate)*up feeding down_proj.
+ * Everything else is the reference's fp32 arithmetic, unchanged. Pinned by
+ * tests/test_oracle.py against a composition of the pinned primitives with
+ * the pinned codec at exactly those points. */
 void orc_model_set_f16_mirror(orc_model* m, int on);
+/* Noise-floor mode, also not the reference: the forward's matvecs add their
+ * products in descending index order (bias first, as the reference does).
+ * Comparing a run with its ascending twin measures how far the result moves
+ * under a change of fp32 summation order alone -- the floor any other
+ * correct implementation (a GPU's tree of partial sums) can be held to.
+ * Pinned like the mirror mode, against the primitives on reversed inputs. */
+void orc_model_set_descending_sums(orc_model* m, int on);
 
 orc_seq* orc_seq_new(const orc_model* m, uint32_t max_tokens);
 void orc_seq_free(orc_seq* s);

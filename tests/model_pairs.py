@@ -67,3 +67,43 @@ def rel_err(a, b):
 def top2_gap(logits):
     s = np.sort(np.asarray(logits, np.float64))
     return float(s[-1] - s[-2])
+
+
+def dequant_oracle(cfg, mode, seed=0, threads=16, sigma=0.02):
+    """The oracle the synthetic hip model is checked against, built in place
+    (no fp32 copy of the source weights): untied, every GEMV weight (and the
+    LM head, the embedding when tied) the dequantized product of the
+    backend's quantizer on the seeded synthetic weights; embedding, norms and
+    biases exact."""
+    ucfg = dataclasses.replace(cfg, tie_word_embeddings=False)
+    m = O.OracleModel(ucfg, threads)
+    for kind, layer, arr in m.tensors():
+        if kind in NORM_KINDS:
+            arr[...] = 1.0
+            continue
+        src_kind = O.T_EMBED if (kind == O.T_LM_HEAD and cfg.tie_word_embeddings) else kind
+        arr[...] = O.synth_normal(seed, src_kind * 1000 + layer, arr.size, sigma).reshape(arr.shape)
+        if kind in GEMV_KINDS or kind == O.T_LM_HEAD:
+            arr[...] = O.quant_dequant(arr, mode)
+    return m
+
+
+def oracle_run(ref, prompt, steps, mirror, forced=None, descending=False):
+    """Logits after the prompt and after each of `steps` tokens (greedy on
+    the oracle's own logits, or the `forced` tokens), and the tokens fed.
+    descending: the noise-floor twin (matvec products added in descending
+    order)."""
+    ref.set_f16_mirror(mirror)
+    ref.set_descending_sums(descending)
+    s = ref.new_seq(len(prompt) + steps + 1)
+    code, b = ref.prefill(s, prompt)
+    assert code == 0
+    traj, toks = [b], []
+    for i in range(steps):
+        toks.append(O.argmax(b) if forced is None else forced[i])
+        code, b = ref.decode(s, toks[-1])
+        assert code == 0
+        traj.append(b)
+    ref.set_f16_mirror(False)
+    ref.set_descending_sums(False)
+    return traj, toks

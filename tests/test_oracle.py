@@ -287,3 +287,160 @@ def test_threaded_matvec_bit_identical():
     x = rng.standard_normal(700).astype(np.float32)
     b = rng.standard_normal(1000).astype(np.float32)
     np.testing.assert_array_equal(O.matvec(w, x, b, threads=1), O.matvec(w, x, b, threads=7))
+
+
+def test_threaded_attention_bit_identical():
+    rng = np.random.default_rng(6)
+    heads, kvh, hd, ctx = 28, 4, 128, 300
+    q = rng.standard_normal(heads * hd).astype(np.float32)
+    k = rng.standard_normal((ctx, kvh * hd)).astype(np.float32)
+    v = rng.standard_normal((ctx, kvh * hd)).astype(np.float32)
+    np.testing.assert_array_equal(O.attention(q, k, v, heads, kvh, hd),
+                                  O.attention(q, k, v, heads, kvh, hd, threads=5))
+
+
+def test_model_threads_bit_identical():
+    """The forward with matvec rows and attention heads spread over threads
+    equals the single-threaded forward (which equals oracle/_ref) bit for bit;
+    the context is long enough for the threaded attention path."""
+    cfg = O.QwenConfig(512, 256, 1, 8, 2, 64, 512, 700, 1e-6, 1e6, False, 511)
+    outs = []
+    for threads in (1, 6):
+        m = O.OracleModel(cfg, threads)
+        fill_synthetic(m, seed=4)
+        s = m.new_seq(cfg.max_context_tokens)
+        code, logits = m.prefill(s, list(O.synth_tokens(3, 0, 600, cfg.vocab_size)))
+        assert code == 0
+        outs.append(logits)
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+# ------------------------------------------------------------ fp16 mirror
+_LIBM = None
+
+
+def _expf(x):
+    """glibc's expf, the function the oracle's SiLU calls."""
+    global _LIBM
+    import ctypes
+    if _LIBM is None:
+        _LIBM = ctypes.CDLL("libm.so.6")
+        _LIBM.expf.restype, _LIBM.expf.argtypes = ctypes.c_float, [ctypes.c_float]
+    return np.array([_LIBM.expf(float(v)) for v in x], np.float32)
+
+
+def _descending(w, x, b=None):
+    """orc_matvec with the products added in descending index order: the
+    pinned primitive on reversed columns and input."""
+    return O.matvec(np.ascontiguousarray(w[:, ::-1]), np.ascontiguousarray(x[::-1]), b)
+
+
+def _mirror_composition(m, tokens, matvec=O.matvec, mirror=True):
+    """One sequence through qwen_model.cpp:212-331, composed from the pinned
+    primitives (orc_matvec, orc_rmsnorm, orc_rope, orc_attention), with the
+    pinned fp16 codec applied at exactly the five mirror points (none when
+    mirror is False). Logits after every token."""
+    c = m.cfg
+    r16 = O.round_f16 if mirror else (lambda v: v)
+    O_matvec = matvec
+    hd, nq, nkv = c.head_dim, c.num_heads, c.num_kv_heads
+    T = lambda kind, l=0: m.tensor(kind, l)
+    keys = [np.zeros((len(tokens), nkv * hd), np.float32) for _ in range(c.num_layers)]
+    vals = [np.zeros((len(tokens), nkv * hd), np.float32) for _ in range(c.num_layers)]
+    out = []
+    for pos, tok in enumerate(tokens):
+        hidden = T(O.T_EMBED)[tok].copy()
+        for l in range(c.num_layers):
+            x = r16(O.rmsnorm(hidden, T(O.T_INPUT_NORM, l), c.rms_norm_eps))
+            q = O_matvec(T(O.T_Q_W, l), x, T(O.T_Q_B, l))
+            k = O_matvec(T(O.T_K_W, l), x, T(O.T_K_B, l))
+            v = O_matvec(T(O.T_V_W, l), x, T(O.T_V_B, l))
+            q = np.concatenate([O.rope(q[h * hd:(h + 1) * hd], pos, c.rope_theta) for h in range(nq)])
+            k = np.concatenate([O.rope(k[h * hd:(h + 1) * hd], pos, c.rope_theta) for h in range(nkv)])
+            keys[l][pos], vals[l][pos] = r16(k), r16(v)
+            attn = r16(O.attention(q, keys[l][:pos + 1], vals[l][:pos + 1], nq, nkv, hd))
+            hidden = (hidden + O_matvec(T(O.T_O_W, l), attn)).astype(np.float32)
+            x = r16(O.rmsnorm(hidden, T(O.T_POST_NORM, l), c.rms_norm_eps))
+            g = O_matvec(T(O.T_GATE_W, l), x)
+            u = O_matvec(T(O.T_UP_W, l), x)
+            act = r16(g / (np.float32(1.0) + _expf(-g)) * u)
+            hidden = (hidden + O_matvec(T(O.T_DOWN_W, l), act)).astype(np.float32)
+        x = r16(O.rmsnorm(hidden, T(O.T_FINAL_NORM), c.rms_norm_eps))
+        head = T(O.T_EMBED) if c.tie_word_embeddings else T(O.T_LM_HEAD)
+        out.append(O_matvec(head, x))
+    return out
+
+
+@pytest.mark.parametrize("cfg", [MID, O.QwenConfig(300, 96, 2, 6, 2, 16, 160, 64, 1e-6, 1e4, True, 299)],
+                         ids=["untied", "tied"])
+def test_f16_mirror_equals_composition_of_pinned_primitives(cfg):
+    """Pins the oracle's fp16 mirror mode: token by token, its logits equal a
+    composition of the already-pinned primitives with fp16 rounding (the
+    pinned codec) at the RMSNorm outputs, the cached K and V, the attention
+    output and SiLU(gate)*up -- bit for bit. Mirror and plain forwards differ
+    (so rounding really happens there) by no more than fp16 rounding can
+    explain."""
+    m = O.OracleModel(cfg, 3)
+    fill_synthetic(m, seed=7)
+    tokens = list(O.synth_tokens(8, 0, 12, cfg.vocab_size))
+    want = _mirror_composition(m, tokens)
+    m.set_f16_mirror(True)
+    s = m.new_seq(64)
+    got = [m.prefill(s, tokens[:1])[1]] + [m.decode(s, t)[1] for t in tokens[1:]]
+    for i, (a, b) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(a, b, err_msg=f"token {i}")
+    m.set_f16_mirror(False)
+    s = m.new_seq(64)
+    plain = [m.prefill(s, tokens[:1])[1]] + [m.decode(s, t)[1] for t in tokens[1:]]
+    d = max(float(np.linalg.norm(a - b) / np.linalg.norm(b)) for a, b in zip(got, plain))
+    assert 0 < d < 1e-2, d
+
+
+def test_parallel_helpers_equal_serial_calls():
+    """The wrapper spreads synthesis and quantization over threads; each
+    equals one serial call of the C function."""
+    import ctypes as C
+    n = (3 << 20) + 77
+    serial = np.empty(n, np.float32)
+    O.lib().orc_synth_normal(9, 1234, 5, n, 0.02, serial.ctypes.data_as(C.c_void_p))
+    np.testing.assert_array_equal(O.synth_normal(9, 1234, n, 0.02, first=5), serial)
+    w = O.synth_normal(1, 2, 700 * 3000, 0.02).reshape(700, 3000)
+    for q, dq, ns in ((O.lib().orc_q4_quantize, O.lib().orc_q4_dequantize, (3000 + 31) // 32),
+                      (O.lib().orc_q8_quantize, O.lib().orc_q8_dequantize, None)):
+        codes = np.empty(w.shape, np.int8)
+        scales = np.empty((700, ns) if ns else (700,), np.uint16)
+        q(w.ctypes.data_as(C.c_void_p), 700, 3000, codes.ctypes.data_as(C.c_void_p),
+          scales.ctypes.data_as(C.c_void_p))
+        out = np.empty(w.shape, np.float32)
+        dq(codes.ctypes.data_as(C.c_void_p), scales.ctypes.data_as(C.c_void_p), 700, 3000,
+           out.ctypes.data_as(C.c_void_p))
+        mode = "int4" if ns else "int8"
+        c2, s2 = O.q4_quantize(w) if ns else O.q8_quantize(w)
+        np.testing.assert_array_equal(c2, codes)
+        np.testing.assert_array_equal(s2, scales)
+        np.testing.assert_array_equal(O.quant_dequant(w, mode), out)
+
+
+@pytest.mark.parametrize("mirror", [False, True], ids=["plain", "mirror"])
+def test_descending_sums_equal_composition_on_reversed_inputs(mirror):
+    """Pins the noise-floor mode: with descending sums the forward equals the
+    composition whose every matvec is the pinned orc_matvec on reversed
+    columns and input, bit for bit; and it differs from the ascending
+    (reference-order) forward by no more than fp32 summation order (plain)
+    or fp16 rounding flips (mirror) can explain."""
+    cfg = MID
+    m = O.OracleModel(cfg, 3)
+    fill_synthetic(m, seed=8)
+    tokens = list(O.synth_tokens(8, 1, 10, cfg.vocab_size))
+    want = _mirror_composition(m, tokens, _descending, mirror)
+    m.set_f16_mirror(mirror)
+    m.set_descending_sums(True)
+    s = m.new_seq(64)
+    got = [m.prefill(s, tokens[:1])[1]] + [m.decode(s, t)[1] for t in tokens[1:]]
+    for i, (a, b) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(a, b, err_msg=f"token {i}")
+    m.set_descending_sums(False)
+    s = m.new_seq(64)
+    asc = [m.prefill(s, tokens[:1])[1]] + [m.decode(s, t)[1] for t in tokens[1:]]
+    d = max(float(np.linalg.norm(a - b) / np.linalg.norm(b)) for a, b in zip(got, asc))
+    assert 0 < d < (5e-3 if mirror else 1e-5), d
