@@ -31,6 +31,7 @@
 // the device's double exp, within an ulp of the host's, which moves a token
 // only when r lies within about 1e-16 of a boundary.
 #include <cmath>
+#include <mutex>
 #include <random>
 
 #include "common.h"
@@ -359,6 +360,72 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __r
     tokens[row] = tok;
 }
 
+// Launches sample_kernel over rows [0, m) with the scratch at `ws` (keys,
+// then probabilities, m * cap 8-byte entries each; every entry a row uses
+// is written before it is read, so the scratch needs no clearing).
+int launch_sample(const float* d_logits, int64_t ldl, int m, int64_t n, float temperature, int32_t top_k,
+                  float top_p, const double* u, int32_t* d_tokens, void* ws, hipStream_t stream) {
+    Draws d{};
+    for (int r = 0; r < m; ++r) {
+        if (!(u[r] >= 0.0 && u[r] < 1.0)) return LYK_ERR_INVALID_ARG;
+        d.u[r] = u[r];
+    }
+    int cap = 1;
+    while (cap < n) cap <<= 1;
+    char* base = static_cast<char*>(ws);
+    uint64_t* keys = reinterpret_cast<uint64_t*>(base);
+    double* probs = reinterpret_cast<double*>(base + (size_t)m * cap * 8);
+    static std::once_flag lds_once;
+    static bool lds_ok = false;
+    std::call_once(lds_once, [] {
+        lds_ok = hipFuncSetAttribute((const void*)sample_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     kLdsKeys * 8) == hipSuccess;
+    });
+    if (!lds_ok) return LYK_ERR_HIP;
+    hipLaunchKernelGGL(sample_kernel, dim3(m), dim3(kSampleThreads), kLdsKeys * 8, stream, d_logits, (int)ldl,
+                       (int)n, temperature, top_k, top_p, d, keys, probs, cap, d_tokens);
+    LYK_LAUNCH_CHECK();
+    return LYK_OK;
+}
+
+int check_sample_args(const float* d_logits, int64_t ldl, int m, int64_t n, float temperature, int32_t top_k,
+                      float top_p, const double* u, const int32_t* d_tokens) {
+    if (!d_logits || !d_tokens || !u || m < 1 || n < 1 || ldl < n || n > (1 << 30)) return LYK_ERR_INVALID_ARG;
+    if (m > kMaxRows) return LYK_ERR_SHAPE;
+    if (!(temperature >= 0.0f) || !std::isfinite(temperature) || !(top_p > 0.0f) || top_p > 1.0f || top_k < 0)
+        return LYK_ERR_INVALID_ARG;
+    return LYK_OK;
+}
+
+// ---------------------------------------------------------- static scratch
+// The allocation-free variant's scratch: a file-scope device array, one copy
+// per GPU the library is loaded on, held until the process ends. Its size
+// covers kMaxRows rows of up to kStaticLogits logits (2^18 >= every Qwen2
+// vocabulary). Host code never passes the array's name to a kernel (on the
+// host it is a stand-in, not a device address): it passes the address
+// hipGetSymbolAddress gave for the current device.
+constexpr int64_t kStaticLogits = 1 << 18;
+constexpr size_t kStaticScratchBytes = (size_t)kMaxRows * kStaticLogits * 16;   // 16 MiB
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices];   // per device, from hipGetSymbolAddress
+
+// The current device's address of `scratch`, looked up on the device's
+// first call; nullptr when the lookup fails.
+void* device_scratch() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        scratch_ptr[dev] = p;
+    }
+    return scratch_ptr[dev];
+}
+
 }  // namespace
 }  // namespace lyk
 
@@ -376,32 +443,22 @@ uint64_t lyk_hip_sample_workspace_bytes(int m, int64_t n) {
 int lyk_hip_sample(const float* d_logits, int64_t ldl, int m, int64_t n, float temperature, int32_t top_k,
                    float top_p, const double* u, int32_t* d_tokens, void* d_workspace, uint64_t workspace_bytes,
                    void* stream) {
-    if (!d_logits || !d_tokens || !u || m < 1 || n < 1 || ldl < n || n > (1 << 30)) return LYK_ERR_INVALID_ARG;
-    if (m > kMaxRows) return LYK_ERR_SHAPE;
-    if (!(temperature >= 0.0f) || !std::isfinite(temperature) || !(top_p > 0.0f) || top_p > 1.0f || top_k < 0)
-        return LYK_ERR_INVALID_ARG;
+    const int rc = check_sample_args(d_logits, ldl, m, n, temperature, top_k, top_p, u, d_tokens);
+    if (rc != LYK_OK) return rc;
     if (!d_workspace || workspace_bytes < lyk_hip_sample_workspace_bytes(m, n)) return LYK_ERR_WORKSPACE;
-    Draws d{};
-    for (int r = 0; r < m; ++r) {
-        if (!(u[r] >= 0.0 && u[r] < 1.0)) return LYK_ERR_INVALID_ARG;
-        d.u[r] = u[r];
-    }
-    int cap = 1;
-    while (cap < n) cap <<= 1;
-    char* base = static_cast<char*>(d_workspace);
-    uint64_t* keys = reinterpret_cast<uint64_t*>(base);
-    double* probs = reinterpret_cast<double*>(base + (size_t)m * cap * 8);
-    static bool lds_set = false;
-    if (!lds_set) {
-        if (hipFuncSetAttribute((const void*)sample_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kLdsKeys * 8) != hipSuccess)
-            return LYK_ERR_HIP;
-        lds_set = true;
-    }
-    hipLaunchKernelGGL(sample_kernel, dim3(m), dim3(kSampleThreads), kLdsKeys * 8, (hipStream_t)stream, d_logits,
-                       (int)ldl, (int)n, temperature, top_k, top_p, d, keys, probs, cap, d_tokens);
-    LYK_LAUNCH_CHECK();
-    return LYK_OK;
+    return launch_sample(d_logits, ldl, m, n, temperature, top_k, top_p, u, d_tokens, d_workspace,
+                         static_cast<hipStream_t>(stream));
+}
+
+int lyk_hip_sample_static(const float* d_logits, int64_t ldl, int m, int64_t n, float temperature, int32_t top_k,
+                          float top_p, const double* u, int32_t* d_tokens, void* stream) {
+    const int rc = check_sample_args(d_logits, ldl, m, n, temperature, top_k, top_p, u, d_tokens);
+    if (rc != LYK_OK) return rc;
+    if (n > kStaticLogits) return LYK_ERR_SHAPE;   // beyond the static scratch
+    void* ws = device_scratch();
+    if (!ws) return LYK_ERR_HIP;
+    return launch_sample(d_logits, ldl, m, n, temperature, top_k, top_p, u, d_tokens, ws,
+                         static_cast<hipStream_t>(stream));
 }
 
 // The draws Sampler takes from its generator: std::mt19937_64 seeded with

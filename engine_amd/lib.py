@@ -63,6 +63,7 @@ _KERNEL_SIGS = {
     "lyk_hip_gemm_q": (I, [P, I64, I64, I64, P, P, I64, I, I, P, P, I64, P]),
     "lyk_hip_sample_workspace_bytes": (U64, [I, I64]),
     "lyk_hip_sample": (I, [P, I64, I, I64, C.c_float, C.c_int32, C.c_float, P, P, P, U64, P]),
+    "lyk_hip_sample_static": (I, [P, I64, I, I64, C.c_float, C.c_int32, C.c_float, P, P, P]),
     "lyk_rng_new": (P, [U64]),
     "lyk_rng_free": (None, [P]),
     "lyk_rng_canonical": (C.c_double, [P]),

@@ -264,6 +264,17 @@ int lyk_hip_sample(const float* d_logits, int64_t ldl, int m, int64_t n,
                    float temperature, int32_t top_k, float top_p,
                    const double* u, int32_t* d_tokens, void* d_workspace,
                    uint64_t workspace_bytes, void* stream);
+/* lyk_hip_sample without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * scratch is a file-scope device array of 16 MiB (4 rows of up to 2^18
+ * logits), one per GPU the library runs on, held until the process ends;
+ * n > 2^18 returns LYK_ERR_SHAPE. Nothing is allocated or freed. Calls that
+ * overlap in time on one GPU (different streams, no ordering between them)
+ * share that scratch and race; calls on one stream are ordered and do not. */
+int lyk_hip_sample_static(const float* d_logits, int64_t ldl, int m, int64_t n,
+                          float temperature, int32_t top_k, float top_p,
+                          const double* u, int32_t* d_tokens, void* stream);
 /* The generator Sampler draws from (sampler.cpp:32-33): std::mt19937_64
  * seeded with the request's seed; lyk_rng_canonical returns the next
  * generate_canonical<double, 53> draw, the u of lyk_hip_sample. */
