@@ -97,6 +97,7 @@ struct StepArgs {
     int phases;             // phases of one launch (trace layout)
     int pf_off;             // LDS byte offset of the gate/up staging region
     int pf_chunks;          // gate/up chunks per wave staged there (0: none)
+    int o_grid;             // workgroups of the o phase: the lowest o_grid of the grid
     uint64_t spin_ticks;    // a wait gives up after this many s_memrealtime ticks
 };
 
@@ -288,9 +289,11 @@ struct Part {
     bool busy;
 };
 
-__device__ __forceinline__ Part partition(const Mat& A) {
+// G: the workgroups the phase spreads over, from blockIdx 0 (the whole grid
+// but for o, which keeps off the top of the grid where attention units run).
+__device__ __forceinline__ Part partition(const Mat& A, int G) {
     Part p;
-    const int G = gridDim.x, b = blockIdx.x;
+    const int b = blockIdx.x;
     p.pieces = tile_pieces(A.tiles, A.chunks, G);
     if (p.pieces == 1) {
         p.gp = A.tiles < G ? A.tiles : G;
@@ -490,7 +493,7 @@ __device__ __forceinline__ void stage_gateup(const StepArgs& a, const lyk_step_l
     extern __shared__ __align__(16) unsigned char smem[];
     const Mat A = make_mat<Q8>(Lw.gateup_w, Lw.gateup_s, a.md.intermediate_size, a.md.hidden_size, true,
                                a.md.tile_rows[2]);
-    const Part p = partition(A);
+    const Part p = partition(A, gridDim.x);
     if (!p.busy) return;
     const int tid = phase_tid();
     const int lane = tid & 63, wave = uniform(tid >> 6);
@@ -518,23 +521,30 @@ __device__ __forceinline__ void stage_gateup(const StepArgs& a, const lyk_step_l
 
 // ------------------------------------------------------------ phase inputs
 
-// Residual rows (registers, element i = tid + j*kThreads of each row) plus
-// the tagged block output d[m*H + i] of this layer, polled.
+// Inputs are fetched by resumable pollers: attempt() makes one pass over
+// the words still missing (one memory round trip) and returns how many
+// remain, so a phase can make its first attempt before queueing any weight
+// load of its own (a load waits behind every load its CU issued before it).
+
+// The tagged block output d[m*H + i] of this layer for the thread's
+// residual elements (i = tid + j*kThreads of each row), added to the
+// residual rows by apply().
 template <int M>
-__device__ __forceinline__ bool residual_add(const StepArgs& a, float (&h)[M][kNormPer], const u64* d,
-                                             uint32_t tag, int tid) {
-    const int H = a.md.hidden_size;
+struct ResidualIn {
     // rows in batches of up to two: word u = (j, row m0 + u % RB) of a batch
-    constexpr int RB = M < 2 ? M : 2, NB = (M + RB - 1) / RB;
+    static constexpr int RB = M < 2 ? M : 2, NB = (M + RB - 1) / RB;
     static_assert(kNormPer * 2 <= 32, "residual batch");
-    uint32_t want = 0, have[NB];
-#pragma unroll
-    for (int j = 0; j < kNormPer; ++j)
-        if (tid + j * kThreads < H) want |= ((1u << RB) - 1) << (j * RB);
-#pragma unroll
-    for (int q = 0; q < NB; ++q) have[q] = 0;
+    uint32_t want, have[NB];
     float add[M][kNormPer];
-    auto pending = [&]() {
+    __device__ __forceinline__ void init(int H, int tid) {
+        want = 0;
+#pragma unroll
+        for (int j = 0; j < kNormPer; ++j)
+            if (tid + j * kThreads < H) want |= ((1u << RB) - 1) << (j * RB);
+#pragma unroll
+        for (int q = 0; q < NB; ++q) have[q] = 0;
+    }
+    __device__ __forceinline__ int attempt(const u64* d, uint32_t tag, int H, int tid) {
         int missing = 0;
 #pragma unroll
         for (int q = 0; q < NB; ++q) {
@@ -550,15 +560,54 @@ __device__ __forceinline__ bool residual_add(const StepArgs& a, float (&h)[M][kN
                 });
         }
         return missing;
-    };
-    if (!spin(a, pending)) return false;
+    }
+    __device__ __forceinline__ void apply(float (&h)[M][kNormPer], int H, int tid) const {
 #pragma unroll
-    for (int j = 0; j < kNormPer; ++j)
-        if (tid + j * kThreads < H)
+        for (int j = 0; j < kNormPer; ++j)
+            if (tid + j * kThreads < H)
 #pragma unroll
-            for (int m = 0; m < M; ++m) h[m][j] += add[m][j];
-    return true;
-}
+                for (int m = 0; m < M; ++m) h[m][j] += add[m][j];
+    }
+};
+
+// A window of n tagged words per row, src[m] + e for e < n (entries at or
+// past `valid` read as 0): the thread's words e = tid + u*kThreads, u <
+// kWinWords (the host keeps windows within kThreads * kWinWords words).
+constexpr int kWinWords = 8;
+template <int M>
+struct WindowIn {
+    uint32_t want[M], have[M], v[M][kWinWords];
+    __device__ __forceinline__ void init(int n, int valid, int tid) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            want[m] = have[m] = 0;
+#pragma unroll
+            for (int u = 0; u < kWinWords; ++u) {
+                const int e = tid + u * kThreads;
+                v[m][u] = 0;
+                if (e < n && e < valid) want[m] |= 1u << u;
+            }
+        }
+    }
+    template <class Src>
+    __device__ __forceinline__ int attempt(Src src, int valid, uint32_t tag, int tid) {
+        int missing = 0;
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            missing += poll_batch<kWinWords>(want[m], have[m], tag,
+                                             [&](int u) { return src(m) + min(tid + u * kThreads, valid - 1); },
+                                             [&](int u, uint32_t x) { v[m][u] = x; });
+        return missing;
+    }
+    template <class Out>
+    __device__ __forceinline__ void finish(int n, int tid, Out out) const {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int u = 0; u < kWinWords; ++u)
+                if (tid + u * kThreads < n) out(m, tid + u * kThreads, v[m][u]);
+    }
+};
 
 // The gamma values of this thread's residual elements that fall in the
 // workgroup's window, requested before the residual poll so that their
@@ -615,72 +664,6 @@ __device__ __forceinline__ void norm_window(const StepArgs& a, const float (&h)[
     }
 }
 
-// Polls words src[0..n) (a word past `valid` reads as 0) into out(i, payload),
-// KB words per thread per round trip, so a window of up to 512*KB words costs
-// one memory round trip once its producers have written it.
-template <int KB, class Out>
-__device__ __forceinline__ bool poll_words(const StepArgs& a, const u64* src, int n, int valid, uint32_t tag,
-                                           int tid, Out out) {
-    bool ok = true;
-    for (int e0 = tid; e0 < n; e0 += kThreads * KB) {
-        uint32_t v[KB];
-        uint32_t want = 0, have = 0;
-#pragma unroll
-        for (int u = 0; u < KB; ++u) {
-            const int e = e0 + u * kThreads;
-            v[u] = 0;
-            if (e < n && e < valid) want |= 1u << u;
-        }
-        auto pending = [&]() {
-            return poll_batch<KB>(want, have, tag, [&](int u) { return src + min(e0 + u * kThreads, valid - 1); },
-                                  [&](int u, uint32_t x) { v[u] = x; });
-        };
-        ok = spin(a, pending) && ok;
-#pragma unroll
-        for (int u = 0; u < KB; ++u) {
-            const int e = e0 + u * kThreads;
-            if (e < n) out(e, v[u]);
-        }
-    }
-    return ok;
-}
-
-// x window <- fp16 of the tagged fp32 attention outputs [M][nq*hd] of the
-// window's chunks.
-template <int M, bool Q8>
-__device__ __forceinline__ bool fill_attn(const StepArgs& a, uint32_t tag, const Mat& A, const Part& p,
-                                          uint16_t* xs, int tid) {
-    if (!p.busy) return true;
-    const int CK = A.ck, kq = a.md.num_heads * a.md.head_dim;
-    const int n = p.win * CK, k0 = p.ca * CK;
-    bool ok = true;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        uint16_t* dst = xs + (size_t)m * n;
-        ok = poll_words<8>(a, a.attn_out + (size_t)m * kq + k0, n, kq - k0, tag, tid,
-                           [&](int e, uint32_t v) { dst[e] = f2h(bitsf(v)); }) && ok;
-    }
-    return ok;
-}
-
-// x window <- the tagged SiLU(gate) * up pairs of the window's chunks.
-template <int M, bool Q8>
-__device__ __forceinline__ bool fill_act(const StepArgs& a, uint32_t tag, const Mat& A, const Part& p,
-                                         uint16_t* xs, int tid) {
-    if (!p.busy) return true;
-    const int W = A.ck / 2;  // pairs per chunk
-    const int In2 = a.md.intermediate_size / 2;
-    const int n = p.win * W, i0 = p.ca * W;
-    bool ok = true;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        uint32_t* dst = reinterpret_cast<uint32_t*>(xs) + (size_t)m * n;
-        ok = poll_words<8>(a, a.act + (size_t)m * In2 + i0, n, In2 - i0, tag, tid,
-                            [&](int e, uint32_t v) { dst[e] = v; }) && ok;
-    }
-    return ok;
-}
-
 struct Best {
     float v;
     int i;
@@ -725,7 +708,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     const Mat A = make_mat<Q8>(wp, sp, n, k, kind == kGateUp, a.md.tile_rows[slot]);
     const int CK = A.ck;
     mark(a, ph, 0);
-    const Part p = partition(A);
+    const Part p = partition(A, kind == kOut ? a.o_grid : (int)gridDim.x);
     const int b = blockIdx.x;
     const int lane = tid & 63, wave = uniform(tid >> 6);
     const int len = p.f1 - p.f0;
@@ -741,49 +724,71 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     const unsigned char* pfb = smem + a.pf_off + wave * a.pf_chunks * kSlotBytes<Q8>;
     if (npf > 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // The wave's first two register chunks are requested before the inputs
-    // are polled (streamed while waiting), the next two once they are in:
-    // the polls queue behind the loads issued before them, so the prefetch
-    // ahead of them is kept short.
-    u32x4 wa[kChunkBlocks], wb[kChunkBlocks], wc[kChunkBlocks], wd[kChunkBlocks];
-    u64 sa = 0, sb = 0, sc = 0, sd = 0;
+    // ---- inputs: the residual's block output (normed phases) or the
+    // polled window (o, down), fetched by resumable pollers
+    const bool normed = kind == kQkv || kind == kGateUp || kind == kHead;
+    const u64* d = nullptr;   // the block output the residual adds (normed phases)
+    uint32_t dtag = 0;
+    const float* gamma = a.md.final_norm;
+    if (kind == kQkv) {
+        if (l > 0) {
+            d = a.d_mlp + (size_t)(l - 1) * kMaxRows * H;
+            dtag = tag - 1;
+        }
+        gamma = Lw.input_norm;
+    } else if (kind == kGateUp) {
+        d = a.d_attn + (size_t)l * kMaxRows * H;
+        dtag = tag;
+        gamma = Lw.post_norm;
+    } else if (kind == kHead) {
+        d = a.d_mlp + (size_t)(L - 1) * kMaxRows * H;
+        dtag = tag - 1;
+    }
+    float gv[kNormPer];
+    if (normed) load_gamma(a, gamma, A, p, tid, gv);
+    // o: fp32 attention outputs [M][nq*hd]; down: SiLU(gate) * up fp16 pairs
+    // [M][In/2]; the window of chunks [ca, ca + win)
+    const int wlen = kind == kDown ? CK / 2 : CK;
+    const int wn = p.win * wlen, w0e = p.ca * wlen;
+    const int wtot = kind == kDown ? In / 2 : nq * hd;
+    const u64* wsrc = kind == kDown ? a.act : a.attn_out;
+    auto wrow = [&](int m) { return wsrc + (size_t)m * wtot + w0e; };
+    ResidualIn<M> rin;
+    WindowIn<M> win;
+    auto attempt = [&]() -> int {
+        if (normed) return d ? rin.attempt(d, dtag, H, tid) : 0;
+        return p.busy ? win.attempt(wrow, wtot - w0e, tag, tid) : 0;
+    };
+    if (normed) {
+        if (d) rin.init(H, tid);
+    } else if (p.busy) {
+        win.init(wn, wtot - w0e, tid);
+    }
+    // The wave's first two weight chunks are requested before the inputs
+    // are polled (they stream while it waits); the stream then keeps two
+    // chunks in flight per wave. (Polling first and requesting only when an
+    // input is missing was measured slower: the late workgroups then wait
+    // out the chunks' latency after their inputs. Four chunks in flight was
+    // slower too: 32 MB of requests queued across the grid delay every poll
+    // and partial-sum read behind them, and the workgroups that finish a
+    // phase last wait longest.)
+    u32x4 wa[kChunkBlocks], wb[kChunkBlocks];
+    u64 sa = 0, sb = 0;
     if (g0 < w1) CM::load(A, g0, nv_of(g0), lane, wa, sa);
     if (g0 + 1 < w1) CM::load(A, g0 + 1, nv_of(g0 + 1), lane, wb, sb);
-
-    // ---- inputs
-    bool ok = true;
-    if (kind == kQkv || kind == kGateUp || kind == kHead) {
-        // residual += the block output this norm follows, then RMSNorm
-        const u64* d = nullptr;
-        uint32_t dtag = 0;
-        const float* gamma;
-        if (kind == kQkv) {
-            if (l > 0) {
-                d = a.d_mlp + (size_t)(l - 1) * kMaxRows * H;
-                dtag = tag - 1;
-            }
-            gamma = Lw.input_norm;
-        } else if (kind == kGateUp) {
-            d = a.d_attn + (size_t)l * kMaxRows * H;
-            dtag = tag;
-            gamma = Lw.post_norm;
-        } else {
-            d = a.d_mlp + (size_t)(L - 1) * kMaxRows * H;
-            dtag = tag - 1;
-            gamma = a.md.final_norm;
-        }
-        float gv[kNormPer];
-        load_gamma(a, gamma, A, p, tid, gv);
-        if (d) ok = residual_add<M>(a, h, d, dtag, tid);
-        if (ok && p.busy) norm_window<M, Q8>(a, h, gv, A, p, xs, tid);
-    } else if (kind == kOut) {
-        ok = fill_attn<M, Q8>(a, tag, A, p, xs, tid);
-    } else {
-        ok = fill_act<M, Q8>(a, tag, A, p, xs, tid);
-    }
-    if (g0 + 2 < w1) CM::load(A, g0 + 2, nv_of(g0 + 2), lane, wc, sc);
-    if (g0 + 3 < w1) CM::load(A, g0 + 3, nv_of(g0 + 3), lane, wd, sd);
+    const bool ok = spin(a, attempt);
+    // one decision for the workgroup before any code with barriers
     if (block_any(!ok)) return false;
+    if (normed) {
+        if (d) rin.apply(h, H, tid);
+        if (p.busy) norm_window<M, Q8>(a, h, gv, A, p, xs, tid);
+    } else if (p.busy) {
+        if (kind == kDown)
+            win.finish(wn, tid, [&](int m, int e, uint32_t v) { reinterpret_cast<uint32_t*>(xs)[(size_t)m * wn + e] = v; });
+        else
+            win.finish(wn, tid, [&](int m, int e, uint32_t v) { xs[(size_t)m * wn + e] = f2h(bitsf(v)); });
+    }
+    __syncthreads();   // the x window is complete before any wave reads it
     mark(a, ph, 1);
     if (!p.busy) {
         mark(a, ph, 2);
@@ -828,7 +833,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         if constexpr (Q8) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
         const int cend = p.pieces == 1 ? A.chunks : p.f1 - t * A.chunks;
         // One chunk: math on the buffer, then (register chunks) request the
-        // chunk four ahead into it; a tile's sums go to its piece slot when
+        // chunk two ahead into it; a tile's sums go to its piece slot when
         // the tile ends.
         auto step = [&](u32x4 (&wbuf)[kChunkBlocks], u64& sbuf, bool refill) -> bool {
             CM::compute(wbuf, sbuf, xs + (size_t)(c - p.ca) * CK + xsub,
@@ -848,7 +853,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                     if (!end) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
             }
             if (end) return true;
-            if (refill && f + 4 < w1) CM::load(A, f + 4, nv_of(f + 4), lane, wbuf, sbuf);
+            if (refill && f + 2 < w1) CM::load(A, f + 2, nv_of(f + 2), lane, wbuf, sbuf);
             __builtin_amdgcn_sched_barrier(0);
             ++f;
             c = c + 1 == A.chunks ? 0 : c + 1;
@@ -864,8 +869,6 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         while (!done) {
             if (step(wa, sa, true)) break;
             if (step(wb, sb, true)) break;
-            if (step(wc, sc, true)) break;
-            if (step(wd, sd, true)) break;
         }
     }
     __syncthreads();  // every wave is done with the x window
@@ -1730,6 +1733,21 @@ struct PhaseShape {
     int64_t tiles, chunks, range, win, ck;  // range: chunks of one workgroup, at most
     int pieces;
 };
+// Workgroups of the o phase at `rows` rows: those below the attention units,
+// which fill the grid from the top (at most rows * nkv * max_splits of
+// them), so that no workgroup runs both; the whole grid when that leaves
+// fewer than a quarter of it.
+int o_phase_grid(const lyk_step_model& md, int rows, int grid) {
+    const int splits = md.attn_max_splits ? md.attn_max_splits : kAttnDefaultSplits;
+    const int64_t units = (int64_t)rows * md.num_kv_heads * splits;
+    const int64_t og = grid - units;
+    return og >= grid / 4 ? (int)og : grid;
+}
+// The grid phase i (0 qkv, 1 o, 2 gate/up, 3 down, 4 head) spreads over.
+int phase_grid(const lyk_step_model& md, int i, int rows, int grid) {
+    return i == 1 ? o_phase_grid(md, rows, grid) : grid;
+}
+
 PhaseShape phase_shape(const MatShape& mt, bool q8, int grid) {
     PhaseShape ps;
     tiled_shape(mt.n, mt.k, mt.paired, q8, mt.tr, ps.tiles, ps.chunks, ps.ck);
@@ -1758,10 +1776,12 @@ Layout layout(const lyk_step_model& md, int rows, int grid) {
     MatShape mats[5];
     step_mats(md, mats);
     uint64_t dpart_words = 1;
-    for (const MatShape& mt : mats) {
-        const PhaseShape ps = phase_shape(mt, q8, grid);
-        if (ps.pieces > 1) dpart_words = std::max<uint64_t>(dpart_words, (uint64_t)ps.tiles * ps.pieces * rows * 64);
-    }
+    for (int r = 1; r <= rows; ++r)   // the o phase's grid depends on the launch's rows
+        for (int i = 0; i < 5; ++i) {
+            const PhaseShape ps = phase_shape(mats[i], q8, phase_grid(md, i, r, grid));
+            if (ps.pieces > 1)
+                dpart_words = std::max<uint64_t>(dpart_words, (uint64_t)ps.tiles * ps.pieces * rows * 64);
+        }
     L.dpart_stride = (dpart_words * 8 + 255) / 256 * 256 / 8;
     const int64_t head_tiles = (md.vocab_size + md.tile_rows[4] - 1) / md.tile_rows[4];
     uint64_t at = 0;
@@ -1810,7 +1830,8 @@ Staging gateup_staging(const lyk_step_model& md, int rows, int grid) {
     MatShape mats[5];
     step_mats(md, mats);
     Staging sg;
-    sg.off = (int)((std::max(gemv_lds(mats[1], q8, rows, grid), gemv_lds(mats[2], q8, rows, grid)) + 255) / 256 * 256);
+    sg.off = (int)((std::max(gemv_lds(mats[1], q8, rows, o_phase_grid(md, rows, grid)), gemv_lds(mats[2], q8, rows, grid)) +
+                    255) / 256 * 256);
     const int64_t slot = q8 ? 4096 : 4608;
     const PhaseShape ps = phase_shape(mats[2], q8, grid);
     int64_t chunks = ((int64_t)kMaxDynamicLds - sg.off) / (kWaves * slot);
@@ -1827,7 +1848,7 @@ size_t lds_bytes(const lyk_step_model& md, int rows, int grid) {
     MatShape mats[5];
     step_mats(md, mats);
     size_t need = gateup_staging(md, rows, grid).end;
-    for (const MatShape& mt : mats) need = std::max(need, gemv_lds(mt, q8, rows, grid));
+    for (int i = 0; i < 5; ++i) need = std::max(need, gemv_lds(mats[i], q8, rows, phase_grid(md, i, rows, grid)));
     // attention: q high/low parts, chunk weights high/low, current k and v
     // (fp16), current k (fp32), then the larger of the chunk scores, the raw
     // q and the merge's (max, sum) table + partial slice
@@ -1839,13 +1860,21 @@ size_t lds_bytes(const lyk_step_model& md, int rows, int grid) {
     return need;
 }
 
-// Largest number of row tiles one wave's range can touch, over the phases.
+// Whether every phase fits the kernel: a wave's range touches at most
+// kPieces row tiles, and the polled windows of o and down (words per row)
+// fit the window poller.
 bool pieces_ok(const lyk_step_model& md, int grid) {
     const bool q8 = md.q8 != 0;
     MatShape mats[5];
     step_mats(md, mats);
-    for (const MatShape& mt : mats) {
-        const PhaseShape ps = phase_shape(mt, q8, grid);
+    for (int r = 1; r <= kMaxRows; ++r) {
+        const PhaseShape po = phase_shape(mats[1], q8, o_phase_grid(md, r, grid));
+        const PhaseShape pd = phase_shape(mats[3], q8, grid);
+        if (po.win * po.ck > kThreads * kWinWords || pd.win * pd.ck / 2 > kThreads * kWinWords) return false;
+    }
+    for (int i = 0; i < 5; ++i) {
+        const MatShape& mt = mats[i];
+        const PhaseShape ps = phase_shape(mt, q8, phase_grid(md, i, 1, grid));
         const int64_t lw = (ps.range + kWaves - 1) / kWaves;   // chunks per wave, at most
         if (1 + (lw - 1 + ps.chunks - 1) / ps.chunks > kPieces) return false;
     }
@@ -1997,6 +2026,7 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     const Staging sg = gateup_staging(*model, m, grid);
     a.pf_off = sg.off;
     a.pf_chunks = sg.chunks;
+    a.o_grid = o_phase_grid(*model, m, grid);
     hipStream_t st = static_cast<hipStream_t>(stream);
     StepArgs* d_args = reinterpret_cast<StepArgs*>(ws + L.args);
     WorkspaceTable& tab = workspaces();

@@ -44,7 +44,8 @@ typedef struct lyk_model_options {
     /* GEMV tile heights (16/32/64) for qkv, o, gate/up, down, LM head;
      * 0 = lyk_hip_step_tile_rows' choice for this device */
     int32_t tile_rows[5];
-    /* lyk_step_model.lds_prefetch: 0 = as many as fit, -1 = none */
+    /* gate/up chunks per wave staged in LDS during attention: 0 = as many
+     * as fit (the default), -1 = none, n > 0 = at most n */
     int32_t lds_prefetch;
 } lyk_model_options;
 
