@@ -49,6 +49,7 @@ HipModelOptions ToOptions(const lyk_model_options* o) {
     opt.attn_max_splits = o->attn_max_splits;
     for (int i = 0; i < 5; ++i) opt.tile_rows[i] = o->tile_rows[i];
     opt.lds_prefetch = o->lds_prefetch;
+    opt.prefill_chunk = o->prefill_chunk;
     return opt;
 }
 

@@ -316,6 +316,10 @@ struct QwenHipModel::Impl {
     PinnedBuf h_tokens, h_pos, h_tables, h_logits, h_history, h_nonfinite, h_prompt;
     size_t prompt_cap = 0;
 
+    // chunk prefill: prompt rows per pass (0: off) and the pass's buffers
+    uint32_t chunk_rows = 0;
+    DevBuf pf_x, pf_xn, pf_qkv, pf_q, pf_attn, pf_act;
+
     uint64_t prefix_hits = 0;
     uint64_t gemv_bytes = 0;
     bool tracing = false;
@@ -390,6 +394,56 @@ struct QwenHipModel::Impl {
             (void)lyk_hip_step_reset(d_step_ws.p, step_ws_bytes, stream);
             (void)hipStreamSynchronize(stream);
             return Status(ErrorCode::kGpuUnhealthy, "decode step did not complete on the device", kComponent);
+        }
+        return Status::Ok();
+    }
+
+    // One chunk pass over T prompt rows of one sequence (token ids on the
+    // device at d_tok, positions pos0..pos0+T-1, its block table in row 0 of
+    // d_tables, table_len blocks): per layer RMSNorm, the QKV GEMM (+ bias),
+    // RoPE with the K/V append, causal chunk attention, the o GEMM into the
+    // residual, RMSNorm, the gate/up GEMM with SiLU, the down GEMM into the
+    // residual (ForwardChunk, qwen_cuda_model.cu:2398-2516). The last layer
+    // stops after its K/V append: only the prompt's last token, which the
+    // fused step runs, needs the hidden state past it.
+    Status ChunkPass(const int32_t* d_tok, int T, int pos0, int table_len) {
+        const int H = int(c.hidden_size), nq = int(c.num_heads), nkv = int(c.num_kv_heads), hd = int(c.head_dim);
+        const int In = int(c.intermediate_size), kq = nq * hd, rows = (nq + 2 * nkv) * hd;
+        const int bt = int(pool->block_tokens()), nb = int(pool->num_blocks()), qi = q8 ? 1 : 0;
+        const float eps = c.rms_norm_eps;
+        float* X = pf_x.as<float>();
+        uint16_t* Xn = pf_xn.as<uint16_t>();
+        LYK_OK_OR(lyk_hip_embed_rmsnorm(embed.as<float>(), c.vocab_size, d_tok, T, H, X, H,
+                                        layers[0].input_norm.as<float>(), eps, Xn, H, stream),
+                  "prefill embedding failed");
+        for (uint32_t l = 0; l < c.num_layers; ++l) {
+            const Layer& L = layers[l];
+            if (l > 0)
+                LYK_OK_OR(lyk_hip_rmsnorm_f16(X, H, L.input_norm.as<float>(), eps, T, H, Xn, H, stream),
+                          "prefill norm failed");
+            LYK_OK_OR(lyk_hip_gemm_q(Xn, H, T, H, L.qkv.qw.p, L.qkv.qs.p, rows, L.qkv.tile_rows, qi, LYK_GEMM_STORE,
+                                     L.qkv_bias.as<float>(), pf_qkv.p, rows, stream),
+                      "prefill qkv GEMM failed");
+            LYK_OK_OR(lyk_hip_chunk_rope_kv(pf_qkv.as<float>(), rows, T, pos0, nq, nkv, hd, rcos.as<float>(),
+                                            rsin.as<float>(), int(rope_cap), pf_q.as<float>(), kcache(l), vcache(l),
+                                            d_tables.as<int32_t>(), table_len, bt, nb, stream),
+                      "prefill RoPE / KV append failed");
+            if (l + 1 == c.num_layers) break;
+            LYK_OK_OR(lyk_hip_chunk_attention(pf_q.as<float>(), kcache(l), vcache(l), d_tables.as<int32_t>(),
+                                              table_len, T, pos0, nq, nkv, hd, bt, nb, pf_attn.as<uint16_t>(), kq,
+                                              stream),
+                      "prefill attention failed");
+            LYK_OK_OR(lyk_hip_gemm_q(pf_attn.as<uint16_t>(), kq, T, kq, L.o.qw.p, L.o.qs.p, H, L.o.tile_rows, qi,
+                                     LYK_GEMM_ADD, nullptr, X, H, stream),
+                      "prefill o GEMM failed");
+            LYK_OK_OR(lyk_hip_rmsnorm_f16(X, H, L.post_norm.as<float>(), eps, T, H, Xn, H, stream),
+                      "prefill norm failed");
+            LYK_OK_OR(lyk_hip_gemm_q(Xn, H, T, H, L.gateup.qw.p, L.gateup.qs.p, In, L.gateup.tile_rows, qi,
+                                     LYK_GEMM_SILU_PAIRS, nullptr, pf_act.p, In, stream),
+                      "prefill gate/up GEMM failed");
+            LYK_OK_OR(lyk_hip_gemm_q(pf_act.as<uint16_t>(), In, T, In, L.down.qw.p, L.down.qs.p, H, L.down.tile_rows,
+                                     qi, LYK_GEMM_ADD, nullptr, X, H, stream),
+                      "prefill down GEMM failed");
         }
         return Status::Ok();
     }
@@ -649,6 +703,27 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
         return r;
     }
     LOAD_OR_RETURN(I.d_step_ws.Alloc(I.step_ws_bytes, false));
+    // chunk prefill where its kernels take the geometry (head dim 64 or 128,
+    // GEMM rows a multiple of 8)
+    {
+        const uint32_t kq = c.num_heads * c.head_dim;
+        const bool fits = (c.head_dim == 64 || c.head_dim == 128) && H % 8 == 0 && kq % 8 == 0 && In % 8 == 0;
+        const int want = options.prefill_chunk;
+        if (want < -1) {
+            r.status = Status(ErrorCode::kInvalidRequest, "prefill_chunk must be -1, 0 or positive", kComponent);
+            return r;
+        }
+        I.chunk_rows = want == -1 || !fits ? 0u : want == 0 ? 256u : uint32_t(want);
+        if (I.chunk_rows) {
+            const size_t C = I.chunk_rows, rows = size_t(c.num_heads + 2 * c.num_kv_heads) * c.head_dim;
+            LOAD_OR_RETURN(I.pf_x.Alloc(C * H * 4, false));
+            LOAD_OR_RETURN(I.pf_xn.Alloc(C * H * 2, false));
+            LOAD_OR_RETURN(I.pf_qkv.Alloc(C * rows * 4, false));
+            LOAD_OR_RETURN(I.pf_q.Alloc(C * kq * 4, false));
+            LOAD_OR_RETURN(I.pf_attn.Alloc(C * kq * 2, false));
+            LOAD_OR_RETURN(I.pf_act.Alloc(C * In * 2, false));
+        }
+    }
     if (lyk_hip_step_reset(I.d_step_ws.p, I.step_ws_bytes, I.stream) != LYK_OK) {
         r.status = Status(ErrorCode::kGpuUnhealthy, "workspace reset failed", kComponent);
         return r;
@@ -764,9 +839,11 @@ Status QwenHipModel::Prefill(SequenceState& state, const std::vector<uint32_t>& 
 
     Status s = seq.Reserve(n);
     if (!s.ok()) return fail(s);
-    // Tokens and positions of the uncached part go up in one copy; each
-    // step takes its row with a device-to-device copy, so no host staging
-    // buffer is rewritten while a copy from it may be pending.
+    // Tokens and then positions of the uncached part go up in one copy
+    // (rows tokens, rows positions); the chunk passes read the tokens in
+    // place, and each fused step takes its row with device-to-device
+    // copies, so no host staging buffer is rewritten while a copy from it
+    // may be pending.
     const size_t rows = n - start;
     if (rows * 2 > I.prompt_cap) {
         HIP_OK(hipStreamSynchronize(I.stream), "device execution failed");
@@ -776,16 +853,30 @@ Status QwenHipModel::Prefill(SequenceState& state, const std::vector<uint32_t>& 
     }
     int32_t* hp = I.h_prompt.as<int32_t>();
     for (size_t r = 0; r < rows; ++r) {
-        hp[2 * r] = int32_t(tokens[start + r]);
-        hp[2 * r + 1] = int32_t(start + r);
+        hp[r] = int32_t(tokens[start + r]);
+        hp[rows + r] = int32_t(start + r);
     }
     if (hipMemcpyAsync(I.d_prompt.p, hp, rows * 8, hipMemcpyHostToDevice, I.stream) != hipSuccess)
         return fail(Status(ErrorCode::kGpuUnhealthy, "prompt upload failed", kComponent));
     if (!(s = I.UploadRows({&seq}, {tokens[start]}, {start})).ok()) return fail(s);
-    for (uint32_t i = start; i < n; ++i) {
-        const int32_t* row = I.d_prompt.as<int32_t>() + 2 * size_t(i - start);
-        if (hipMemcpyAsync(I.d_tokens.p, row, 4, hipMemcpyDeviceToDevice, I.stream) != hipSuccess ||
-            hipMemcpyAsync(I.d_pos.p, row + 1, 4, hipMemcpyDeviceToDevice, I.stream) != hipSuccess)
+    const int32_t* d_tok = I.d_prompt.as<int32_t>();
+    const int32_t* d_pos = d_tok + rows;
+    // Every token but the last in chunk passes on the matrix cores, the
+    // last through the fused step, which gives the logits; without chunk
+    // passes every token goes through the step (HIDDEN mode but the last).
+    uint32_t first_step = start;
+    if (I.chunk_rows && n - 1 > start) {
+        const int table_len = int(seq.blocks().size());
+        for (uint32_t c0 = start; c0 < n - 1; c0 += I.chunk_rows) {
+            const uint32_t T = std::min(I.chunk_rows, n - 1 - c0);
+            if (!(s = I.ChunkPass(d_tok + (c0 - start), int(T), int(c0), table_len)).ok()) return fail(s);
+        }
+        first_step = n - 1;
+    }
+    for (uint32_t i = first_step; i < n; ++i) {
+        const size_t r = i - start;
+        if (hipMemcpyAsync(I.d_tokens.p, d_tok + r, 4, hipMemcpyDeviceToDevice, I.stream) != hipSuccess ||
+            hipMemcpyAsync(I.d_pos.p, d_pos + r, 4, hipMemcpyDeviceToDevice, I.stream) != hipSuccess)
             return fail(Status(ErrorCode::kGpuUnhealthy, "prompt row copy failed", kComponent));
         if (!(s = I.LaunchStep(1, i + 1 == n ? LYK_STEP_LOGITS : LYK_STEP_HIDDEN)).ok()) return fail(s);
     }

@@ -49,6 +49,10 @@ struct HipModelOptions {
     // Gate/up chunks per wave staged in LDS ahead of the gate/up phase:
     // 0 = as many as fit, -1 = none, n > 0 = at most n.
     int lds_prefetch = 0;
+    // Prompt rows per prefill chunk pass (GEMMs on the matrix cores, causal
+    // chunk attention): 0 = 256, -1 = none (every prompt token through the
+    // fused decode step), n > 0 = n rows.
+    int prefill_chunk = 0;
 };
 
 // fp32 weights by reference tensor name. The safetensors file is one source;

@@ -38,6 +38,29 @@ __device__ __forceinline__ int uniform(int v) {
     return __builtin_amdgcn_readfirstlane(v);
 }
 
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// CPU's RoPE rotation (qwen_model.cpp:49-52) with separately rounded
+// products (no FMA), so equal inputs give equal bits.
+__device__ __forceinline__ float rot_lo(float a, float b, float c, float s) {
+#pragma clang fp contract(off)
+    return a * c - b * s;
+}
+__device__ __forceinline__ float rot_hi(float a, float b, float c, float s) {
+#pragma clang fp contract(off)
+    return b * c + a * s;
+}
+
+// fp32 x as two fp16 parts, hi + lo == x to ~22 bits: an fp16 MFMA of an
+// exact fp16 operand against both parts, accumulated in fp32, keeps the
+// fp32 operand's precision.
+__device__ __forceinline__ void split_f16(float x, uint16_t& hi, uint16_t& lo) {
+    hi = f2h(x);
+    lo = f2h(x - h2f(hi));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -61,17 +61,6 @@ __global__ __launch_bounds__(kThreads) void embed_rmsnorm_kernel(
     rmsnorm_row(dst, gamma, eps, n, xn + (size_t)m * ldx);
 }
 
-// The CPU's rotation a*c - b*s and b*c + a*s with every product rounded
-// separately (no fused multiply-add), so equal inputs give equal bits.
-__device__ __forceinline__ float rot_lo(float a, float b, float c, float s) {
-#pragma clang fp contract(off)
-    return a * c - b * s;
-}
-__device__ __forceinline__ float rot_hi(float a, float b, float c, float s) {
-#pragma clang fp contract(off)
-    return b * c + a * s;
-}
-
 // One workgroup per (head, batch row); head < nq are query heads, then nkv
 // key heads, then nkv value heads. Rotation pairs (i, i + hd/2) use the
 // host-built cos/sin tables, so the products equal the CPU's bit for bit.

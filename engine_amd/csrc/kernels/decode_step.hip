@@ -1037,10 +1037,6 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
 
 // ------------------------------------------------------------ attention
 
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int kTileT = 16;                       // tokens per MFMA tile
 constexpr int kChunkT = 256;                     // tokens per softmax chunk (4 per lane)
 constexpr int kChunkTiles = kChunkT / kTileT;
@@ -1053,24 +1049,6 @@ __device__ __forceinline__ int split_size(int ctx, int split_tokens, int max_spl
     int t = (ctx + max_splits - 1) / max_splits;
     t = (t + kTileT - 1) / kTileT * kTileT;
     return t > split_tokens ? t : split_tokens;
-}
-
-// CPU's rotation with separately rounded products (no FMA).
-__device__ __forceinline__ float rot_lo(float a, float b, float c, float s) {
-#pragma clang fp contract(off)
-    return a * c - b * s;
-}
-__device__ __forceinline__ float rot_hi(float a, float b, float c, float s) {
-#pragma clang fp contract(off)
-    return b * c + a * s;
-}
-
-// fp32 x as two fp16 parts, hi + lo == x to ~22 bits: an fp16 MFMA of an
-// exact fp16 operand against both parts, accumulated in fp32, keeps the
-// fp32 operand's precision.
-__device__ __forceinline__ void split_f16(float x, uint16_t& hi, uint16_t& lo) {
-    hi = f2h(x);
-    lo = f2h(x - h2f(hi));
 }
 
 // Attention units are (row, kv head, context split); the G <= 16 query heads

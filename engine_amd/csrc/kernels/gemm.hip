@@ -1,6 +1,8 @@
-// Prefill GEMM on the matrix cores: Y[T, n] = X[T, K] . W[n, K]^T (+ bias),
-// X fp16, W int4 (groups of 32, fp16 scales) or int8 (fp16 row scales) in the
-// fused step's tiled layout, dequantized on the fly, fp32 accumulation.
+// Prefill GEMM on the matrix cores: Y[T, n] = X[T, K] . W[n, K]^T, X fp16, W
+// int4 (groups of 32, fp16 scales) or int8 (fp16 row scales) in the fused
+// step's tiled layout, fp32 accumulation, with the chunk pass's epilogues:
+// store (+ bias: the QKV sums), add into Y (the residual after o and down),
+// or, for the paired gate/up matrix, fp16 SiLU(gate) * up.
 //
 // Reference: GemmXWtKernel (backends/cuda/qwen_cuda_model.cu:878-908), the
 // prefill GEMM of ForwardChunk (:2398-2516): C = X.W^T + b over a chunk of
@@ -9,15 +11,17 @@
 //
 // A workgroup (4 waves) computes a 128 x 128 tile of Y, each wave a 64 x 64
 // quarter as 4 x 4 accumulators of 16 x 16. Per step of 32 k the workgroup
-// stages in LDS the X tile (fp16) and the W tile dequantized to fp16 (int4:
-// code x group scale, rounded to fp16 once; int8: the code, its row scale
-// applied to the finished sum; the next step's global words are fetched into
+// stages in LDS the X tile (fp16) and the W tile's codes as fp16 (exact: the
+// integers -8..7 or -128..127; the next step's global words are fetched into
 // registers while this step's MFMAs run), then each wave runs 16
 // v_mfma_f32_16x16x32_f16 from LDS operands:
 //   A: lane l holds X[row l % 16][8 (l / 16) .. +7];
 //   B: lane l holds W[column l % 16][8 (l / 16) .. +7].
-// fp32 accumulation. (The fp16 rounding of int4 code x scale is the only
-// rounding before the sum: 2^-12 relative per weight.)
+// A step's 32 k are one int4 group, so its products land in fresh
+// accumulators and join the sums through one fma with the group's scale;
+// int8's row scale multiplies the finished sum. Every product is exact, as
+// in the decode GEMV: the result differs from the dequantized fp32 product
+// by the order of the fp32 additions only.
 #include "common.h"
 
 namespace lyk {
@@ -25,8 +29,6 @@ namespace {
 
 constexpr int kGemmThreads = 256;
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 128;      // rows and columns of Y per workgroup
 constexpr int kRowHalves = 40;  // LDS row of a 32-k slice (fp16), padded against bank conflicts
@@ -37,14 +39,20 @@ __device__ __forceinline__ uint32_t lane_of(int r, int unit, int tr, int& blk) {
     return (uint32_t)((unit % per) * tr + r);
 }
 
-template <bool Q8>
+// Epilogues (the LYK_GEMM_* values of the C ABI).
+constexpr int kStore = 0, kAdd = 1, kSiluPairs = 2;
+
+// ncols: columns of the tiled matrix (rows of W; paired: tiles * tr, the
+// gate and up halves of each tile); n: valid columns (paired: gate rows).
+template <bool Q8, int EP>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __restrict__ x, int ldx, int T, int K,
                                                            const uint8_t* __restrict__ qw,
-                                                           const uint16_t* __restrict__ qs, int n, int tr, int nbp,
-                                                           int nc, const float* __restrict__ bias,
-                                                           float* __restrict__ y, int ldy) {
+                                                           const uint16_t* __restrict__ qs, int n, int ncols, int tr,
+                                                           int nbp, int nc, const float* __restrict__ bias,
+                                                           void* __restrict__ yv, int ldy) {
     __shared__ __align__(16) uint16_t xs[kTile * kRowHalves];
     __shared__ __align__(16) uint16_t ws[kTile * kRowHalves];
+    __shared__ float gsc[kTile];   // int4: this step's group scale per column
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int quad = lane >> 4, col = lane & 15;
     const int t0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
@@ -86,11 +94,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
                 xv1 = u32x4{e[4], e[5], e[6], e[7]};
             }
         }
+        wsc = 0;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int dd = wd + h;   // 8-k slice of the step
             wv[h][0] = wv[h][1] = 0u;
-            if (cn >= n) continue;
+            if (cn >= ncols) continue;
             if constexpr (!Q8) {
                 int blk;
                 const uint32_t l = lane_of(wrr, g, tr, blk);
@@ -106,24 +115,24 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
             }
         }
     };
-    // the fetched words into LDS: X as is, W dequantized
+    // the fetched words into LDS: X as is, W codes as fp16 integers
     auto stage = [&]() {
         u32x4* d = reinterpret_cast<u32x4*>(xs + xr * kRowHalves + 16 * xh);
         d[0] = xv0;
         d[1] = xv1;
+        if constexpr (!Q8)
+            if (wd == 0) gsc[wcol] = h2f(wsc);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int dd = wd + h;
             u32x4 v;
             if constexpr (!Q8) {
-                const _Float16 sc = (_Float16)h2f(wsc);
-                const half2_t s2 = {sc, sc};
                 const uint32_t u = wv[h][0], tt = u >> 8, magic = 0x64006400u;
-                // nibbles of k 8dd+{0,1} | {2,3} (x16) | {4,5} | {6,7} (x16)
-                const half2_t p0 = (as_half2((u & 0x000F000Fu) | magic) + lo_off) * s2;
-                const half2_t p1 = ((as_half2((u & 0x00F000F0u) | magic) + hi_off) * sixteenth) * s2;
-                const half2_t p2 = (as_half2((tt & 0x000F000Fu) | magic) + lo_off) * s2;
-                const half2_t p3 = ((as_half2((tt & 0x00F000F0u) | magic) + hi_off) * sixteenth) * s2;
+                // nibbles of k 8dd+{0,1} | {2,3} (x16, then /16: exact) | {4,5} | {6,7}
+                const half2_t p0 = as_half2((u & 0x000F000Fu) | magic) + lo_off;
+                const half2_t p1 = (as_half2((u & 0x00F000F0u) | magic) + hi_off) * sixteenth;
+                const half2_t p2 = as_half2((tt & 0x000F000Fu) | magic) + lo_off;
+                const half2_t p3 = (as_half2((tt & 0x00F000F0u) | magic) + hi_off) * sixteenth;
                 v = u32x4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
             } else {
                 uint32_t e[4];
@@ -134,7 +143,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
                 }
                 v = u32x4{e[0], e[1], e[2], e[3]};
             }
-            if (cn >= n) v = u32x4{0u, 0u, 0u, 0u};
+            if (cn >= ncols) v = u32x4{0u, 0u, 0u, 0u};
             *reinterpret_cast<u32x4*>(ws + wcol * kRowHalves + 8 * dd) = v;
         }
     };
@@ -151,28 +160,95 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const uint16_t* __re
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             b[j] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(ws + (wc + 16 * j + col) * kRowHalves + 8 * quad));
+        if constexpr (Q8) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        } else {
+            // the group's sums, scaled into the running ones
+            float sg[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sg[j] = gsc[wc + 16 * j + col];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], f32x4{0.0f, 0.0f, 0.0f, 0.0f},
+                                                                           0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(p[e], sg[j], acc[i][j][e]);
+                }
+        }
         __syncthreads();   // the tiles are restaged by the next step
     }
     // D lane l: rows 4 quad + e of the subtile, column l % 16
+    if constexpr (EP == kSiluPairs) {
+        // tile column r < tr/2 is gate row (c / tr) * tr/2 + r, its up row
+        // tr/2 columns on: the next subtile(s) for tr >= 32, 8 lanes on for
+        // tr = 16
+        uint16_t* act = static_cast<uint16_t*>(yv);
+        const int half = tr / 2;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int c = n0 + wc + 16 * j + col;
-        if (c >= n) continue;
-        float s = 1.0f;
-        if constexpr (Q8) s = h2f(ld(qs + (size_t)(c / tr) * 64 + c % tr));
-        const float bb = bias ? ld(bias + c) : 0.0f;
+        for (int j = 0; j < 4; ++j) {
+            const int c = n0 + wc + 16 * j + col;
+            const int r = c % tr, row = c / tr * half + r;
+            // int8: the gate and up rows' scales (the sums are of codes)
+            float sg = 1.0f, su = 1.0f;
+            if constexpr (Q8)
+                if (r < half && c < ncols) {
+                    sg = h2f(ld(qs + (size_t)(c / tr) * 64 + r));
+                    su = h2f(ld(qs + (size_t)(c / tr) * 64 + r + half));
+                }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = t0 + wr + 16 * i + 4 * quad + e;
-                if (t < T) y[(size_t)t * ldy + c] = acc[i][j][e] * s + bb;
-            }
+                for (int e = 0; e < 4; ++e) {
+                    float up;
+                    if (tr == 16) {
+                        up = __shfl_down(acc[i][j][e], 8, 16);
+                    } else {
+                        up = 0.0f;
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj)
+                            if (jj == j + half / 16) up = acc[i][jj][e];
+                    }
+                    const float gt = acc[i][j][e] * sg;
+                    up *= su;
+                    const int t = t0 + wr + 16 * i + 4 * quad + e;
+                    if (r < half && row < n && t < T) act[(size_t)t * ldy + row] = f2h(gt / (1.0f + expf(-gt)) * up);
+                }
+        }
+    } else {
+        float* y = static_cast<float*>(yv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = n0 + wc + 16 * j + col;
+            if (c >= n) continue;
+            float s = 1.0f;
+            if constexpr (Q8) s = h2f(ld(qs + (size_t)(c / tr) * 64 + c % tr));
+            const float bb = EP == kStore && bias ? ld(bias + c) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = t0 + wr + 16 * i + 4 * quad + e;
+                    if (t >= T) continue;
+                    const float v = Q8 ? acc[i][j][e] * s : acc[i][j][e];
+                    float* dst = y + (size_t)t * ldy + c;
+                    if constexpr (EP == kAdd) *dst = *dst + v;
+                    else *dst = v + bb;
+                }
+        }
     }
+}
+
+template <bool Q8>
+void launch_gemm(int ep, dim3 grid, hipStream_t st, const uint16_t* x, int ldx, int T, int K, const uint8_t* qw,
+                 const uint16_t* qs, int n, int ncols, int tr, int nbp, int nc, const float* bias, void* y, int ldy) {
+    auto k = ep == kAdd ? gemm_kernel<Q8, kAdd> : ep == kSiluPairs ? gemm_kernel<Q8, kSiluPairs> : gemm_kernel<Q8, kStore>;
+    hipLaunchKernelGGL(k, grid, dim3(kGemmThreads), 0, st, x, ldx, T, K, qw, qs, n, ncols, tr, nbp, nc, bias, y, ldy);
 }
 
 }  // namespace
@@ -183,24 +259,30 @@ using namespace lyk;
 extern "C" {
 
 int lyk_hip_gemm_q(const uint16_t* d_x, int64_t ldx, int64_t T, int64_t K, const void* d_qw, const void* d_qs,
-                   int64_t n, int tile_rows, int q8, const float* d_bias, float* d_y, int64_t ldy, void* stream) {
+                   int64_t n, int tile_rows, int q8, int epilogue, const float* d_bias, void* d_y, int64_t ldy,
+                   void* stream) {
     if (!d_x || !d_qw || !d_qs || !d_y || T < 1 || K < 1 || n < 1 || ldx < K || ldy < n) return LYK_ERR_INVALID_ARG;
     if (tile_rows != 16 && tile_rows != 32 && tile_rows != 64) return LYK_ERR_INVALID_ARG;
+    if (epilogue != LYK_GEMM_STORE && epilogue != LYK_GEMM_ADD && epilogue != LYK_GEMM_SILU_PAIRS)
+        return LYK_ERR_INVALID_ARG;
     if (T > (1 << 24) || n > (1 << 24) || K > (1 << 24) || ldx % 8) return LYK_ERR_SHAPE;
     // the tiled layout's block and chunk counts per tile (lyk_q*_pack_tiled)
+    const bool paired = epilogue == LYK_GEMM_SILU_PAIRS;
     const int64_t unit = q8 ? 16 : 32, per = 64 / tile_rows;
     const int64_t units = (K + unit - 1) / unit;
     const int64_t nb = (units + per - 1) / per, nc = (nb + 3) / 4, nbp = 4 * nc;
-    dim3 grid((unsigned)((n + kTile - 1) / kTile), (unsigned)((T + kTile - 1) / kTile));
+    const int64_t tiles = paired ? (n + tile_rows / 2 - 1) / (tile_rows / 2) : (n + tile_rows - 1) / tile_rows;
+    const int64_t ncols = paired ? tiles * tile_rows : n;
+    dim3 grid((unsigned)((ncols + kTile - 1) / kTile), (unsigned)((T + kTile - 1) / kTile));
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (q8)
-        hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kGemmThreads), 0, st, d_x, (int)ldx, (int)T, (int)K,
-                           static_cast<const uint8_t*>(d_qw), static_cast<const uint16_t*>(d_qs), (int)n,
-                           tile_rows, (int)nbp, (int)nc, d_bias, d_y, (int)ldy);
+        launch_gemm<true>(epilogue, grid, st, d_x, (int)ldx, (int)T, (int)K, static_cast<const uint8_t*>(d_qw),
+                          static_cast<const uint16_t*>(d_qs), (int)n, (int)ncols, tile_rows, (int)nbp, (int)nc,
+                          d_bias, d_y, (int)ldy);
     else
-        hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kGemmThreads), 0, st, d_x, (int)ldx, (int)T, (int)K,
-                           static_cast<const uint8_t*>(d_qw), static_cast<const uint16_t*>(d_qs), (int)n,
-                           tile_rows, (int)nbp, (int)nc, d_bias, d_y, (int)ldy);
+        launch_gemm<false>(epilogue, grid, st, d_x, (int)ldx, (int)T, (int)K, static_cast<const uint8_t*>(d_qw),
+                           static_cast<const uint16_t*>(d_qs), (int)n, (int)ncols, tile_rows, (int)nbp, (int)nc,
+                           d_bias, d_y, (int)ldy);
     LYK_LAUNCH_CHECK();
     return LYK_OK;
 }

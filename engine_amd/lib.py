@@ -60,7 +60,9 @@ _KERNEL_SIGS = {
     "lyk_hip_attn_decode": (I, [P, P, P, P, I, P, I, I, I, I, I, I, I, P, I64, P, U64, P]),
     "lyk_hip_argmax_workspace_bytes": (U64, [I, I64]),
     "lyk_hip_argmax": (I, [P, I64, I, I64, P, P, P, P, P, P, U64, P]),
-    "lyk_hip_gemm_q": (I, [P, I64, I64, I64, P, P, I64, I, I, P, P, I64, P]),
+    "lyk_hip_gemm_q": (I, [P, I64, I64, I64, P, P, I64, I, I, I, P, P, I64, P]),
+    "lyk_hip_chunk_rope_kv": (I, [P, I64, I, I, I, I, I, P, P, I, P, P, P, P, I, I, I, P]),
+    "lyk_hip_chunk_attention": (I, [P, P, P, P, I, I, I, I, I, I, I, I, P, I64, P]),
     "lyk_hip_sample_workspace_bytes": (U64, [I, I64]),
     "lyk_hip_sample": (I, [P, I64, I, I64, C.c_float, C.c_int32, C.c_float, P, P, P, U64, P]),
     "lyk_hip_sample_static": (I, [P, I64, I, I64, C.c_float, C.c_int32, C.c_float, P, P, P]),
@@ -93,7 +95,8 @@ class ModelOptions(C.Structure):
     _fields_ = [("device_id", C.c_int32), ("kv_pool_tokens", C.c_uint32),
                 ("kv_block_tokens", C.c_uint32), ("quant", C.c_int32),
                 ("attn_split_tokens", C.c_int32), ("attn_max_splits", C.c_int32),
-                ("tile_rows", C.c_int32 * 5), ("lds_prefetch", C.c_int32)]
+                ("tile_rows", C.c_int32 * 5), ("lds_prefetch", C.c_int32),
+                ("prefill_chunk", C.c_int32)]
 
 
 I32P = C.POINTER(C.c_int32)

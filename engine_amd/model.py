@@ -68,11 +68,13 @@ class Options:
     attn_max_splits: int = 0
     tile_rows: tuple = (0, 0, 0, 0, 0)   # qkv, o, gate/up, down, head; 0: device choice
     lds_prefetch: int = 0   # gate/up chunks per wave staged in LDS: 0 as many as fit, -1 none
+    prefill_chunk: int = 0  # prompt rows per chunk pass: 0 = 256, -1 = token by token (fused step)
 
     def c(self):
         return L.ModelOptions(self.device_id, self.kv_pool_tokens, self.kv_block_tokens,
                               1 if self.quant == "int8" else 0, self.attn_split_tokens,
-                              self.attn_max_splits, (C.c_int32 * 5)(*self.tile_rows), self.lds_prefetch)
+                              self.attn_max_splits, (C.c_int32 * 5)(*self.tile_rows), self.lds_prefetch,
+                              self.prefill_chunk)
 
 
 class HipModel:

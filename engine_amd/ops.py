@@ -189,29 +189,66 @@ def sample(logits, temperature, top_k, top_p, u, workspace=None):
     return out
 
 
-def pack_tiled(codes, scales, mode, tile_rows):
-    """The fused step's tiled layout of one (not paired) matrix: (qw, qs) uint8 arrays."""
+def pack_tiled(codes, scales, mode, tile_rows, b_codes=None, b_scales=None):
+    """The fused step's tiled layout of one matrix, or of the pair (codes, b)
+    when b_codes is given (gate and up): (qw, qs) uint8 arrays."""
     n, k = codes.shape
     q8 = mode == "int8"
+    paired = b_codes is not None
     wb, sb = C.c_uint64(), C.c_uint64()
     lay = L.kernels().lyk_q8_layout_tiled if q8 else L.kernels().lyk_q4_layout_tiled
-    L.check("layout_tiled", lay(n, k, 0, tile_rows, C.byref(wb), C.byref(sb)))
+    L.check("layout_tiled", lay(n, k, 1 if paired else 0, tile_rows, C.byref(wb), C.byref(sb)))
     qw = np.zeros(wb.value, np.uint8)
     qs = np.zeros(sb.value, np.uint8)
     pack = L.kernels().lyk_q8_pack_tiled if q8 else L.kernels().lyk_q4_pack_tiled
-    L.check("pack_tiled", pack(_p(np.ascontiguousarray(codes)), _p(np.ascontiguousarray(scales)), None, None,
-                               n, k, tile_rows, _p(qw), _p(qs)))
+    bc = np.ascontiguousarray(b_codes) if paired else None
+    bs = np.ascontiguousarray(b_scales) if paired else None
+    L.check("pack_tiled", pack(_p(np.ascontiguousarray(codes)), _p(np.ascontiguousarray(scales)),
+                               _p(bc) if paired else None, _p(bs) if paired else None, n, k, tile_rows, _p(qw),
+                               _p(qs)))
     return qw, qs
 
 
-def gemm_q(x, qw, qs, n, mode, tile_rows, bias=None):
-    """Y[T, n] = X . W^T (+ bias) on the matrix cores; x fp16 [T, K] on the GPU
-    (row stride a multiple of 8), qw / qs the tiled layout on the GPU."""
+GEMM_STORE, GEMM_ADD, GEMM_SILU_PAIRS = 0, 1, 2
+
+
+def gemm_q(x, qw, qs, n, mode, tile_rows, bias=None, epilogue=GEMM_STORE, y=None):
+    """The prefill GEMM on the matrix cores; x fp16 [T, K] on the GPU (row
+    stride a multiple of 8), qw / qs the tiled layout on the GPU. STORE: Y[T,
+    n] = X . W^T (+ bias), fp32; ADD: y += X . W^T into the given fp32 y;
+    SILU_PAIRS: W paired (gate and up, n rows each), fp16 SiLU(gate) * up."""
     assert x.dtype == torch.float16 and x.dim() == 2 and x.stride(1) == 1
     T, K = x.shape
-    y = torch.empty(T, n, dtype=torch.float32, device=x.device)
+    if y is None:
+        assert epilogue != GEMM_ADD
+        dt = torch.float16 if epilogue == GEMM_SILU_PAIRS else torch.float32
+        y = torch.empty(T, n, dtype=dt, device=x.device)
+    assert y.stride(1) == 1 and y.shape[0] == T
     L.check("lyk_hip_gemm_q", L.kernels().lyk_hip_gemm_q(_p(x), x.stride(0), T, K, _p(qw), _p(qs), n, tile_rows,
-                                                         1 if mode == "int8" else 0,
-                                                         _p(bias) if bias is not None else None, _p(y), n,
+                                                         1 if mode == "int8" else 0, epilogue,
+                                                         _p(bias) if bias is not None else None, _p(y), y.stride(0),
                                                          stream_ptr()))
     return y
+
+
+def chunk_rope_kv(qkv, pos0, nq, nkv, hd, cos, sin, kcache, vcache, table, block_tokens):
+    """Chunk prefill RoPE + KV append (lyk_hip_chunk_rope_kv): qkv fp32 [T,
+    (nq+2nkv)*hd] at positions pos0..; returns q rotated, fp32 [T, nq*hd]; K/V
+    go into the caches (fp16, [blocks][nkv][bt][hd] and [blocks][nkv][hd][bt])
+    through table (int32 block ids). cos/sin fp32 [max_pos, hd/2]."""
+    T = qkv.shape[0]
+    q = torch.empty(T, nq * hd, dtype=torch.float32, device=qkv.device)
+    L.check("lyk_hip_chunk_rope_kv", L.kernels().lyk_hip_chunk_rope_kv(
+        _p(qkv), qkv.stride(0), T, pos0, nq, nkv, hd, _p(cos), _p(sin), cos.shape[0], _p(q), _p(kcache),
+        _p(vcache), _p(table), table.numel(), block_tokens, kcache.shape[0], stream_ptr()))
+    return q
+
+
+def chunk_attention(q, pos0, nq, nkv, hd, kcache, vcache, table, block_tokens):
+    """Chunk prefill causal attention (lyk_hip_chunk_attention): fp16 [T, nq*hd]."""
+    T = q.shape[0]
+    out = torch.empty(T, nq * hd, dtype=torch.float16, device=q.device)
+    L.check("lyk_hip_chunk_attention", L.kernels().lyk_hip_chunk_attention(
+        _p(q), _p(kcache), _p(vcache), _p(table), table.numel(), T, pos0, nq, nkv, hd, block_tokens,
+        kcache.shape[0], _p(out), out.stride(0), stream_ptr()))
+    return out

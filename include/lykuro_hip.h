@@ -239,15 +239,48 @@ int lyk_hip_argmax(const float* d_logits, int64_t ldl, int m, int64_t n,
                    int32_t* d_history, int32_t* d_step, void* d_workspace,
                    uint64_t workspace_bytes, void* stream);
 
-/* Prefill GEMM on the matrix cores: d_y[t][j] = sum_k x[t][k] * W[j][k]
- * (+ d_bias[j]) for t < T, j < n; x fp16 [T][ldx] (ldx a multiple of 8), W
- * one matrix of n rows (not paired) in the tiled layout above with tile height
- * tile_rows (q8: int8), y fp32 [T][ldy]. Replaces GemmXWtKernel
- * (backends/cuda/qwen_cuda_model.cu:878-908), the chunk GEMM of prefill. */
+/* Prefill GEMM on the matrix cores over a chunk of T prompt rows: x fp16
+ * [T][ldx] (ldx a multiple of 8) times W^T, W in the tiled layout above with
+ * tile height tile_rows (q8: int8), fp32 sums whose products are exact (the
+ * codes times fp16 x; int4 group scales and int8 row scales applied to the
+ * sums). Epilogues, for j < n:
+ *   LYK_GEMM_STORE       y fp32 [T][ldy]: y[t][j] = sum (+ d_bias[j])
+ *   LYK_GEMM_ADD         y fp32 [T][ldy]: y[t][j] += sum (the residual)
+ *   LYK_GEMM_SILU_PAIRS  W paired (gate rows A, up rows B, n each), y fp16
+ *                        [T][ldy]: y[t][j] = fp16(SiLU(gate_j) * up_j)
+ * Replaces GemmXWtKernel and the epilogue kernels of ForwardChunk
+ * (backends/cuda/qwen_cuda_model.cu:878-908, 2398-2516). */
+#define LYK_GEMM_STORE 0
+#define LYK_GEMM_ADD 1
+#define LYK_GEMM_SILU_PAIRS 2
 int lyk_hip_gemm_q(const uint16_t* d_x, int64_t ldx, int64_t T, int64_t K,
                    const void* d_qw, const void* d_qs, int64_t n, int tile_rows,
-                   int q8, const float* d_bias, float* d_y, int64_t ldy,
-                   void* stream);
+                   int q8, int epilogue, const float* d_bias, void* d_y,
+                   int64_t ldy, void* stream);
+
+/* Chunk prefill, RoPE + KV append: T rows of one sequence's raw qkv sums
+ * (fp32 [T][ldq], [q | k | v], bias included) at positions pos0 .. pos0+T-1;
+ * q rotated into d_q fp32 [T][nq*hd], k rotated and v appended as fp16 to the
+ * fused step's paged caches (K [blk][nkv][bt][hd], V [blk][nkv][hd][bt])
+ * through d_table (table_len block ids). cos/sin as for
+ * lyk_hip_rope_kv_append. Replaces ForwardChunk's RoPE and KV scatter
+ * (backends/cuda/qwen_cuda_model.cu:822-870, 2398-2516). */
+int lyk_hip_chunk_rope_kv(const float* d_qkv, int64_t ldq, int T, int pos0,
+                          int nq, int nkv, int hd, const float* d_cos,
+                          const float* d_sin, int max_pos, float* d_q,
+                          uint16_t* d_kcache, uint16_t* d_vcache,
+                          const int32_t* d_table, int table_len,
+                          int block_tokens, int num_blocks, void* stream);
+/* Chunk prefill, causal attention: the T queries of d_q (rows at positions
+ * pos0..) over the cached keys 0..pos of each, out fp16 [T][ldo] =
+ * softmax(q k^T / sqrt(hd)) v per head, kv head = head / (nq/nkv); hd 64 or
+ * 128, block_tokens a multiple of 16. Replaces ChunkAttentionKernel
+ * (backends/cuda/qwen_cuda_model.cu:981-1030). */
+int lyk_hip_chunk_attention(const float* d_q, const uint16_t* d_kcache,
+                            const uint16_t* d_vcache, const int32_t* d_table,
+                            int table_len, int T, int pos0, int nq, int nkv,
+                            int hd, int block_tokens, int num_blocks,
+                            uint16_t* d_out, int64_t ldo, void* stream);
 
 /* Temperature / top-k / top-p sampling per row, Sampler::Sample's rule
  * (core/generation/sampler.cpp:35-106; replaces the host sort the engine runs
