@@ -9,18 +9,30 @@ chained by GreedyRun. Weights are random-init N(0, 0.02) (synthetic, no
 checkpoint) quantized at load; the prompt is P uniform random token ids.
 One JSON line is printed:
   value        decode tokens/s (whole job; one GPU)
+  prefill      time to first token of the P-token prompt (chunk passes on the
+               matrix cores, then the last token through the fused step)
+  phases       one traced step after the timed ones: per layer-phase span (us,
+               mean over the middle layers) and GB/s of its weights, and the
+               GEMV time-weighted fraction of peak (sum of the GEMV phases'
+               weight bytes / sum of their spans / 8 TB/s)
   roofline     the dominant (only) kernel of a step, decode_step_kernel:
                algorithmic HBM bytes of one launch (packed GEMV weights and
                scales + K/V of the context, fp16) / its average duration,
                from HIP events on the model's stream around the timed steps
   cpu_baseline the reference engine's own CPU QwenModel (oracle/_ref), single
                thread as the reference runs it, on a bounded sample (see
-               cpu_baseline.sample); the C restatement (oracle) if _ref is absent
+               cpu_baseline.sample) at the GPU run's mean context; the C
+               restatement (oracle) if _ref is absent
   roofline.traffic  HBM bytes per launch measured by rocprofv3 (FETCH_SIZE +
                WRITE_SIZE, calibrated on a plain copy), read from
                profiles/decode_step_traffic.json when that file was measured on
                the same kernel and workload (bench_profile.py writes it); else null
 Only N=1 is supported: this build targets one GPU.
+
+  python bench.py --gemv
+times the isolated INT4 GEMV kernel (gemv.hip) at the four Qwen2.5-7B shapes
+of BASELINE config 2, M = 1, 2, 4, rotating over >= 512 MB of weight copies
+(2x the 256 MB MALL) so that every call reads HBM; one JSON line.
 
   python bench.py --copy-calibration
 copies 1 GiB device to device 4 times (the runtime's plain copy kernel): the
@@ -63,10 +75,17 @@ def run_decode(args):
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, cfg.vocab_size, args.prompt).astype(np.uint32)
     seq = hip.new_seq(args.prompt + args.warmup + args.steps + 8)
-    t0 = time.time()
+    # a warm-up prefill of another sequence first (first-launch costs)
+    warm = hip.new_seq(64)
+    assert hip.prefill(warm, prompt[:40])[0] == 0
+    warm.close()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     code, logits = hip.prefill(seq, prompt)
+    torch.cuda.synchronize()
+    ttft = time.perf_counter() - t0
     assert code == 0, f"prefill failed with code {code}"
-    log(f"[bench] prefill {args.prompt} tokens {time.time() - t0:.1f}s")
+    log(f"[bench] prefill {args.prompt} tokens {ttft * 1e3:.1f} ms ({args.prompt / ttft:.0f} tok/s)")
     tok = int(np.argmax(logits))
 
     def greedy(n, tok):
@@ -97,9 +116,62 @@ def run_decode(args):
     kv_per_ctx = cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
     step_bytes = hip.gemv_weight_bytes + kv_per_ctx * (ctx0 + ctx + 1) / 2
     gemv_bytes = hip.gemv_weight_bytes
+    phases = phase_breakdown(hip, seq, tok, cfg, args.quant)
     hip.close()
-    return dict(tok_s=args.steps / dt, ms=dt * 1e3 / args.steps, ctx_end=ctx, kernel_us=kernel_us,
-                step_bytes=step_bytes, gemv_bytes=gemv_bytes, tokens=toks)
+    return dict(tok_s=args.steps / dt, ms=dt * 1e3 / args.steps, ctx_end=ctx, ctx_mean=(ctx0 + ctx) / 2,
+                kernel_us=kernel_us, step_bytes=step_bytes, gemv_bytes=gemv_bytes, tokens=toks,
+                ttft_ms=ttft * 1e3, phases=phases)
+
+
+def phase_breakdown(hip, seq, tok, cfg, quant):
+    """One traced GreedyRun step: per phase kind, the mean span over the
+    middle layers (from the previous phase done on every workgroup to this
+    one done on every workgroup; the spans of a step add up to the step),
+    the bytes the phase must read (its packed weights and scales; attention:
+    K and V of the context) and their rate; the LM head alone."""
+    from engine_amd import lib as L
+    import ctypes as C
+    k = L.kernels()
+    q8 = 1 if quant == "int8" else 0
+    H, In, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    kq, kvd = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+
+    def packed(n, kk, paired, normed):
+        tr = k.lyk_hip_step_tile_rows(n, kk, paired, q8, normed)
+        wb, sb = C.c_uint64(), C.c_uint64()
+        lay = k.lyk_q8_layout_tiled if q8 else k.lyk_q4_layout_tiled
+        L.check("layout_tiled", lay(n, kk, paired, tr, C.byref(wb), C.byref(sb)))
+        return wb.value + sb.value
+
+    ctx = seq.length + 1
+    nbytes = {"qkv": packed(kq + 2 * kvd, H, 0, 1), "attn": 2 * ctx * kvd * 2, "o": packed(H, kq, 0, 0),
+              "gate_up": packed(In, H, 1, 1), "down": packed(H, In, 0, 0), "lm_head": packed(V, H, 0, 1)}
+    hip.set_step_tracing(True)
+    code, _ = hip.greedy_run(seq, tok, 1)
+    assert code == 0
+    grid = k.lyk_hip_step_grid()
+    Lyr = cfg.num_layers
+    nph = 5 * Lyr + 2
+    tr = hip.step_trace()[: grid * (4 * nph + 2)].reshape(grid, 4 * nph + 2).astype(np.int64)
+    hip.set_step_tracing(False)
+    t0 = tr[:, 0].min()
+    done = (tr[:, 2:].reshape(grid, nph, 4)[:, :, 3].max(0) - t0) / 100.0   # us (100 MHz)
+    names = ["qkv", "attn", "o", "gate_up", "down"]
+    out = {}
+    for j, n in enumerate(names):
+        spans = [done[5 * l + j] - done[5 * l + j - 1] for l in range(2, Lyr - 1)]
+        us = float(np.mean(spans))
+        out[n] = {"us": round(us, 2), "bytes": nbytes[n], "gbs": round(nbytes[n] / (us * 1e3), 1)}
+    us = float(done[5 * Lyr] - done[5 * Lyr - 1])
+    out["lm_head"] = {"us": round(us, 2), "bytes": nbytes["lm_head"], "gbs": round(nbytes["lm_head"] / (us * 1e3), 1)}
+    gemv = ["qkv", "o", "gate_up", "down"]
+    gb = sum(out[n]["bytes"] for n in gemv) * Lyr + out["lm_head"]["bytes"]
+    gt = sum(out[n]["us"] for n in gemv) * Lyr + out["lm_head"]["us"]
+    return {"per_layer": out, "step_us_traced": round(float(done[nph - 1]), 1),
+            "gemv_time_weighted_gbs": round(gb / (gt * 1e3), 1),
+            "gemv_time_weighted_frac": round(gb / (gt * 1e3) / PEAK_HBM_GBS, 4),
+            "note": "spans from the in-kernel trace of one traced step (mean of layers 2..L-2); "
+                    "the GEMV fraction weights each GEMV phase by its time"}
 
 
 def copy_calibration():
@@ -128,63 +200,156 @@ def measured_traffic(kernel, workload):
 
 
 # ----------------------------------------------------------- CPU baseline
-def cpu_baseline(tokens=3):
-    """Reference QwenModel (oracle/_ref) on the 7B architecture, single thread,
-    with 1 and then 2 decoder layers; per-token time extrapolated to 28
-    layers as t(1) + 27 * (t(2) - t(1)). Weights are random fp16 in a
-    safetensors file (values do not change CPU time); the head is tied to the
-    embedding, the same [152064, 3584] matvec as the untied 7B head."""
+def cpu_info():
+    """The host CPU's model string and the cores this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return model, usable
+
+
+def _ref_or_port(cfg, tensors_fn, use_ref):
+    """The reference QwenModel (oracle/_ref) on weights tensors_fn() writes
+    to a safetensors file (fp16: values do not change CPU time), or the C
+    restatement with the same fill when _ref is absent."""
+    from oracle import oracle as O
+    if use_ref:
+        path = os.path.join(tempfile.gettempdir(), f"lyk_cpu_baseline_{os.getpid()}.safetensors")
+        O.write_safetensors(path, tensors_fn(), dtype="F16")
+        m = O.RefModel(cfg, path)
+        os.remove(path)
+        return m
+    m = O.OracleModel(cfg, threads=1)
+    t = tensors_fn()
+    for kind, layer, arr in m.tensors():
+        arr[...] = t[O.tensor_name(kind, layer)]
+    return m
+
+
+def cpu_baseline(context, tokens=3):
+    """Reference QwenModel (oracle/_ref) on the 7B architecture, single
+    thread, per decode token at `context`:
+      * the per-token time at a short context, from 1- and 2-layer models
+        extrapolated to 28 layers as t(1) + 27 * (t(2) - t(1)) (the head is
+        tied to the embedding: the same [152064, 3584] matvec as the untied
+        7B head);
+      * plus 28 x the attention time that `context` cached tokens add to one
+        layer, measured on a 1-layer model with the 7B attention geometry (28
+        q / 4 kv heads of 128) and a narrow residual (hidden 64, MLP 16,
+        vocab 256), prefilled to `context` tokens: decode at `context`
+        minus decode at a short context.
+    Weights are random fp16; the prompt tokens are random."""
     from oracle import oracle as O
     from engine_amd.model import QWEN25_7B
     import dataclasses
 
     use_ref = O.ref_available()
-    base = O.QwenConfig(**{**dataclasses.asdict(QWEN25_7B), "max_context_tokens": 64,
-                           "tie_word_embeddings": True})
     rng = np.random.default_rng(2)
     block = (rng.standard_normal(1 << 24).astype(np.float32) * 0.02)
-    times = {}
-    for layers in (1, 2):
-        cfg = dataclasses.replace(base, num_layers=layers)
-        if use_ref:
-            tensors = {}
+
+    def weights(cfg):
+        def fn():
+            out = {}
             names = [("model.embed_tokens.weight", cfg.shape(O.T_EMBED)),
                      ("model.norm.weight", cfg.shape(O.T_FINAL_NORM))]
-            for l in range(layers):
+            for l in range(cfg.num_layers):
                 for kind, suffix in O.LAYER_NAMES.items():
                     names.append((f"model.layers.{l}.{suffix}", cfg.shape(kind)))
             for name, shape in names:
                 cnt = int(np.prod(shape))
-                if "norm" in name:
-                    tensors[name] = np.ones(shape, np.float32)
-                else:
-                    reps = -(-cnt // block.size)
-                    tensors[name] = np.tile(block, reps)[:cnt].reshape(shape)
-            path = os.path.join(tempfile.gettempdir(), f"lyk_cpu_baseline_{layers}.safetensors")
-            O.write_safetensors(path, tensors, dtype="F16")
-            del tensors
-            m = O.RefModel(cfg, path)
-            os.remove(path)
-        else:
-            m = O.OracleModel(cfg, threads=1)
-            for kind, layer, arr in m.tensors():
-                arr[...] = 1.0 if kind in (O.T_INPUT_NORM, O.T_POST_NORM, O.T_FINAL_NORM) else \
-                    np.resize(block, arr.size).reshape(arr.shape)
-        s = m.new_seq(16)
-        code, logits = m.prefill(s, [1])
+                out[name] = np.ones(shape, np.float32) if "norm" in name else \
+                    np.tile(block, -(-cnt // block.size))[:cnt].reshape(shape)
+            return out
+        return fn
+
+    def per_token(m, max_tokens, prompt):
+        s = m.new_seq(max_tokens)
+        code, _ = m.prefill(s, prompt)
+        assert code == 0
         t0 = time.perf_counter()
         for i in range(tokens):
-            code, logits = m.decode(s, 2 + i)
-        times[layers] = (time.perf_counter() - t0) / tokens
-        del m, s
-    per_layer = times[2] - times[1]
-    t_token = times[1] + 27 * per_layer
+            code, _ = m.decode(s, 2 + i)
+            assert code == 0
+        return (time.perf_counter() - t0) / tokens
+
+    base = O.QwenConfig(**{**dataclasses.asdict(QWEN25_7B), "max_context_tokens": 64, "tie_word_embeddings": True})
+    times = {}
+    for layers in (1, 2):
+        cfg = dataclasses.replace(base, num_layers=layers)
+        m = _ref_or_port(cfg, weights(cfg), use_ref)
+        times[layers] = per_token(m, 16, [1])
+        del m
+    t_short = times[1] + 27 * (times[2] - times[1])
+    narrow = dataclasses.replace(base, num_layers=1, hidden_size=64, intermediate_size=16, vocab_size=256,
+                                 eos_token_id=255, max_context_tokens=context + tokens + 8)
+    m = _ref_or_port(narrow, weights(narrow), use_ref)
+    a_short = per_token(m, 16, [1])
+    a_long = per_token(m, context + tokens + 8, [int(t) for t in rng.integers(0, 256, context)])
+    del m
+    t_token = t_short + QWEN25_7B.num_layers * max(a_long - a_short, 0.0)
+    model, usable = cpu_info()
     return dict(value=round(1.0 / t_token, 4), unit="tok/s", cores=1,
-                kind="reference" if use_ref else "port",
+                kind="reference" if use_ref else "port", cpu=model, nproc=usable, context=context,
                 sample=(f"Qwen2.5-7B-architecture decode on the {'reference QwenModel (oracle/_ref)' if use_ref else 'C restatement (oracle)'}, "
-                        f"single thread, {tokens} tokens each with 1 and 2 layers "
-                        f"({times[1]:.2f}s, {times[2]:.2f}s per token); 28 layers extrapolated: "
-                        f"{t_token:.2f}s per token"))
+                        f"single thread, {tokens} tokens each: 1- and 2-layer models at context 2 "
+                        f"({times[1]:.2f}s, {times[2]:.2f}s per token; 28 layers extrapolated: {t_short:.2f}s), "
+                        f"plus 28 x the attention cost of {context} cached tokens per layer "
+                        f"({(a_long - a_short) * 1e3:.1f} ms, narrow 1-layer model with the 7B heads): "
+                        f"{t_token:.2f}s per token at context {context}"))
+
+
+def gemv_bench(quant):
+    """Isolated GEMV (gemv.hip, lyk_hip_gemv_q4/q8) at BASELINE config 2's
+    Qwen2.5-7B shapes, M = 1, 2, 4, fp16 N(0, 1) activations, weights N(0,
+    0.02) quantized; each call reads the next of R weight copies totalling
+    >= 512 MB (2x the MALL), so the rate is HBM's. >= 100 timed calls per
+    case with HIP events; GB/s = packed weight + scale bytes per call / its
+    average time."""
+    import torch
+    from engine_amd import ops
+    shapes = {"gate_up": (18944, 3584), "down": (3584, 18944), "qkv": (4608, 3584), "lm_head": (152064, 3584)}
+    rng = np.random.default_rng(0)
+    cases = []
+    for name, (n, k) in shapes.items():
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        base = ops.PackedWeight.from_float(quant, w)
+        del w
+        reps = max(2, -(-(512 << 20) // base.nbytes))
+        copies = [base] + [ops.PackedWeight(quant, n, k, base.qw.cpu().numpy(), base.qs.cpu().numpy())
+                           for _ in range(reps - 1)]
+        for m in (1, 2, 4):
+            x = torch.randn(m, ops.padded_k(k, quant), dtype=torch.float16, device="cuda")
+            y = torch.empty(m, n, dtype=torch.float32, device="cuda")
+            for c in copies[:2]:
+                ops.gemv(c, x, y=y)
+            iters = max(100, 2 * reps)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(iters):
+                ops.gemv(copies[i % reps], x, y=y)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / iters
+            gbs = base.nbytes / (us * 1e3)
+            cases.append({"shape": name, "n": n, "k": k, "m": m, "us": round(us, 2), "bytes": base.nbytes,
+                          "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4), "copies": reps})
+            log(f"[gemv] {name} n={n} k={k} M={m}: {us:.1f} us, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS * 100:.1f}%)")
+        del copies, base
+        torch.cuda.empty_cache()
+    print(json.dumps({"metric": f"isolated {quant.upper()} GEMV HBM GB/s (BASELINE config 2, Qwen2.5-7B shapes)",
+                      "unit": "GB/s", "peak": PEAK_HBM_GBS, "kernel": "gemv.hip (lyk_hip_gemv_q4/q8)",
+                      "rotation_bytes_min": 512 << 20, "cases": cases}), flush=True)
 
 
 def prefill_gemm(quant):
@@ -266,6 +431,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--prefill-gemm", action="store_true", help="time the prefill GEMM instead (one JSON line)")
     ap.add_argument("--sample", action="store_true", help="time device sampling instead (one JSON line)")
+    ap.add_argument("--gemv", action="store_true", help="time the isolated GEMV at config 2 instead (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -283,6 +449,9 @@ def main():
     if args.sample:
         sample_bench()
         return
+    if args.gemv:
+        gemv_bench(args.quant)
+        return
     dec = run_decode(args)
     achieved = dec["step_bytes"] / (dec["kernel_us"] * 1e-6) / 1e9
     log(f"[bench] decode {dec['tok_s']:.1f} tok/s ({dec['ms']:.3f} ms/token wall, {dec['kernel_us']:.1f} us/step "
@@ -294,7 +463,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
-        cpu = cpu_baseline()
+        cpu = cpu_baseline(int(round(dec["ctx_mean"])))
         log(f"[bench] cpu baseline {cpu['value']} tok/s ({time.time() - t0:.1f}s)")
     line = {
         "metric": "decode tok/s Qwen2.5-7B INT4 bs=1 on 1 MI355X; GEMV HBM GB/s vs peak",
@@ -317,6 +486,11 @@ def main():
             "context_at_end": dec["ctx_end"],
             "quant": args.quant,
         },
+        "prefill": {"tokens": args.prompt, "ttft_ms": round(dec["ttft_ms"], 1),
+                    "tok_s": round(args.prompt / dec["ttft_ms"] * 1e3, 1),
+                    "path": "chunk passes of 256 rows (MFMA GEMMs, causal chunk attention), last token through "
+                            "the fused step"},
+        "phases": dec["phases"],
         "roofline": roof,
         "roofline_kernel": {"kernel": kernel, "workload": workload,
                             "avg_us": round(dec["kernel_us"], 2),

@@ -14,9 +14,8 @@ time limit:
      copies): factor = 1 GiB / counter reading, which scales 2.
 Writes <out>/decode_step_kernel_trace.md, <out>/decode_step_traffic.md and
 <out>/decode_step_traffic.json (read by bench.py for roofline.traffic).
-rocprofv3 can exit with a segmentation fault after the profiled program has
-finished when kernels are launched cooperatively; a pass whose program
-printed its JSON line and whose output files exist is used.
+Every pass must end with rocprofv3's exit status 0; any other status fails
+the run, whatever the profiled program printed.
 """
 from __future__ import annotations
 
@@ -49,10 +48,11 @@ def rocprof(tag, prof_args, bench_args, tmp, limit):
     # profiler) passes through
     r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, text=True)
     lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
-    if not lines:
+    if r.returncode != 0 or not lines:
         log(r.stdout[-2000:])
-        raise SystemExit(f"[profile] {tag}: the profiled program did not finish (rc {r.returncode})")
-    log(f"[profile] {tag}: done (rocprofv3 rc {r.returncode})")
+        raise SystemExit(f"[profile] {tag}: rocprofv3 exited with status {r.returncode}"
+                         + ("" if lines else " before the program printed its line"))
+    log(f"[profile] {tag}: done (rocprofv3 exit status 0)")
     return out, json.loads(lines[-1]), " ".join(["rocprofv3", *prof_args, "--", "python3", "bench.py", *bench_args])
 
 
@@ -92,7 +92,7 @@ def main():
     dur = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in timed]
     total = sum(float(r["TotalDurationNs"]) for r in stats)
     md = ["# decode_step_kernel: kernel trace of the bench command", "",
-          f"Command (from the repo root, on one MI355X): `{cmd_trace}`", "",
+          f"Command (from the repo root, on one MI355X): `{cmd_trace}` (rocprofv3 exit status 0)", "",
           "bench.py line of this run:", "", "```", json.dumps(line), "```", "",
           "rocprofv3 --stats (every dispatch of the run, prefill included):", "",
           "| kernel | calls | total ms | avg us | share |", "|---|---:|---:|---:|---:|"]

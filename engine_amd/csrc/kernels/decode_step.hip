@@ -65,7 +65,8 @@ constexpr int kPieces = 4;           // row tiles one wave's range may touch
 constexpr int kNormPer = 10;         // hidden_size <= kNormPer * kThreads
 constexpr int kMaxRows = 4;
 constexpr int kAttnMaxSplits = 64;   // context splits per (row, kv head), at most (a lane each in the merge)
-constexpr int kAttnDefaultSplits = 32;   // the default cap: more units than the grid has workgroups idle in QKV wait on QKV work
+constexpr int kAttnDefaultSplits = 32;   // the default cap, at most (attn_splits_cap)
+constexpr int kAttnMinDefaultSplits = 8;  // and at least
 constexpr int kAttnSplitTokens = 32; // default: tokens per split, at least
 constexpr int kChunkBlocks = 4;      // 16-byte blocks per lane in a GEMV chunk
 constexpr int kMinPieceChunks = 4;   // K chunks per piece of a split tile, at least
@@ -1711,15 +1712,48 @@ struct PhaseShape {
     int64_t tiles, chunks, range, win, ck;  // range: chunks of one workgroup, at most
     int pieces;
 };
+// Attention splits per (row, kv head), at most: the model's setting, else as
+// many as the workgroups with no QKV tile can take, within
+// [kAttnMinDefaultSplits, kAttnDefaultSplits]. A unit on a workgroup with a
+// QKV tile starts its K/V loads and q poll only once that tile is done
+// (measured at 7B, one row, 116 units: those units' q arrived 8 us after
+// QKV was done everywhere, against 2 us for the others, and the phase took
+// 17.5 us instead of 11).
+PhaseShape phase_shape(const MatShape& mt, bool q8, int grid);
+int attn_splits_cap(const lyk_step_model& md, int rows, int grid) {
+    if (md.attn_max_splits) return md.attn_max_splits;
+    MatShape mats[5];
+    step_mats(md, mats);
+    const PhaseShape q = phase_shape(mats[0], md.q8 != 0, grid);
+    const int64_t busy = q.pieces == 1 ? std::min<int64_t>(q.tiles, grid) : q.tiles * q.pieces;
+    const int64_t cap = (grid - busy) / ((int64_t)rows * md.num_kv_heads);
+    return (int)std::clamp<int64_t>(cap, kAttnMinDefaultSplits, kAttnDefaultSplits);
+}
+
+// Whether GEMV phase i (0 qkv, 1 o, 2 gate/up, 3 down, 4 head) of matrix mt
+// spread over G workgroups keeps within the kernel's limits: the polled
+// input window of o (fp32 words) and down (fp16 pairs) within kThreads *
+// kWinWords words (the RMSNorm-fed phases hold the whole residual instead),
+// and each wave's chunk range within kPieces row tiles.
+bool phase_fits(const MatShape& mt, bool q8, int G, int i) {
+    const PhaseShape ps = phase_shape(mt, q8, G);
+    if ((i == 1 || i == 3) && ps.win * ps.ck / (i == 3 ? 2 : 1) > kThreads * kWinWords) return false;
+    const int64_t lw = (ps.range + kWaves - 1) / kWaves;   // chunks per wave, at most
+    return 1 + (lw - 1 + ps.chunks - 1) / ps.chunks <= kPieces;
+}
+
 // Workgroups of the o phase at `rows` rows: those below the attention units,
 // which fill the grid from the top (at most rows * nkv * max_splits of
 // them), so that no workgroup runs both; the whole grid when that leaves
-// fewer than a quarter of it.
+// fewer than a quarter of it or o does not fit on fewer workgroups.
 int o_phase_grid(const lyk_step_model& md, int rows, int grid) {
-    const int splits = md.attn_max_splits ? md.attn_max_splits : kAttnDefaultSplits;
+    const int splits = attn_splits_cap(md, rows, grid);
     const int64_t units = (int64_t)rows * md.num_kv_heads * splits;
     const int64_t og = grid - units;
-    return og >= grid / 4 ? (int)og : grid;
+    if (og < grid / 4) return grid;
+    MatShape mats[5];
+    step_mats(md, mats);
+    return phase_fits(mats[1], md.q8 != 0, (int)og, 1) ? (int)og : grid;
 }
 // The grid phase i (0 qkv, 1 o, 2 gate/up, 3 down, 4 head) spreads over.
 int phase_grid(const lyk_step_model& md, int i, int rows, int grid) {
@@ -1845,17 +1879,9 @@ bool pieces_ok(const lyk_step_model& md, int grid) {
     const bool q8 = md.q8 != 0;
     MatShape mats[5];
     step_mats(md, mats);
-    for (int r = 1; r <= kMaxRows; ++r) {
-        const PhaseShape po = phase_shape(mats[1], q8, o_phase_grid(md, r, grid));
-        const PhaseShape pd = phase_shape(mats[3], q8, grid);
-        if (po.win * po.ck > kThreads * kWinWords || pd.win * pd.ck / 2 > kThreads * kWinWords) return false;
-    }
-    for (int i = 0; i < 5; ++i) {
-        const MatShape& mt = mats[i];
-        const PhaseShape ps = phase_shape(mt, q8, phase_grid(md, i, 1, grid));
-        const int64_t lw = (ps.range + kWaves - 1) / kWaves;   // chunks per wave, at most
-        if (1 + (lw - 1 + ps.chunks - 1) / ps.chunks > kPieces) return false;
-    }
+    for (int r = 1; r <= kMaxRows; ++r)
+        for (int i = 0; i < 5; ++i)
+            if (!phase_fits(mats[i], q8, phase_grid(md, i, r, grid), i)) return false;
     return true;
 }
 
@@ -1998,7 +2024,7 @@ int lyk_hip_decode_step(const lyk_step_model* model, const lyk_step_io* io, void
     a.dpart_stride = (size_t)L.dpart_stride;
     a.best = reinterpret_cast<u64*>(ws + L.best);
     a.attn_split_tokens = model->attn_split_tokens ? model->attn_split_tokens : kAttnSplitTokens;
-    a.attn_max_splits = model->attn_max_splits ? model->attn_max_splits : kAttnDefaultSplits;
+    a.attn_max_splits = attn_splits_cap(*model, m, grid);
     a.phases = (int)lyk_hip_step_phases(model, io->mode);
     a.spin_ticks = model->wait_limit_us ? (uint64_t)model->wait_limit_us * 100u : kSpinTicks;
     const Staging sg = gateup_staging(*model, m, grid);
