@@ -68,7 +68,8 @@ def run_decode(args):
 
     cfg = M.QWEN25_7B
     t0 = time.time()
-    opts = M.Options(quant=args.quant, kv_pool_tokens=args.prompt + args.warmup + args.steps + 512)
+    opts = M.Options(quant=args.quant, kv_pool_tokens=args.prompt + args.warmup + args.steps + 512,
+                     prefill_chunk=args.prefill_chunk)
     hip = M.HipModel.synthetic(cfg, seed=0, sigma=0.02, options=opts)
     log(f"[bench] load (synthetic 7B, {args.quant}) {time.time() - t0:.1f}s, "
         f"GEMV bytes/token {hip.gemv_weight_bytes / 1e9:.3f} GB")
@@ -427,6 +428,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--quant", choices=["int4", "int8"], default="int4")
+    ap.add_argument("--prefill-chunk", type=int, default=0, help="prompt rows per prefill chunk pass (0: default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--prefill-gemm", action="store_true", help="time the prefill GEMM instead (one JSON line)")
@@ -488,7 +490,7 @@ def main():
         },
         "prefill": {"tokens": args.prompt, "ttft_ms": round(dec["ttft_ms"], 1),
                     "tok_s": round(args.prompt / dec["ttft_ms"] * 1e3, 1),
-                    "path": "chunk passes of 256 rows (MFMA GEMMs, causal chunk attention), last token through "
+                    "path": "chunk passes of up to 2048 rows (MFMA GEMMs, causal chunk attention), last token through "
                             "the fused step"},
         "phases": dec["phases"],
         "roofline": roof,

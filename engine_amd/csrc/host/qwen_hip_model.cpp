@@ -31,6 +31,11 @@ namespace {
 
 constexpr const char kComponent[] = "qwen_hip";
 constexpr int kMaxBatch = 4;          // rows per fused step (lyk_hip_decode_step limit)
+// prompt rows per prefill chunk pass by default: a 2048-token prompt in one
+// pass fills the grid in every GEMM (measured at 7B: 256 rows 320 ms, 1024
+// rows 110 ms, 2048 rows 79 ms to the first token); chunk sizes do not change
+// the results (no row's arithmetic depends on its chunk)
+constexpr uint32_t kDefaultChunkRows = 2048;
 constexpr uint32_t kGreedyMax = 256;  // greedy steps per GreedyRun call
 
 Status HipFail(hipError_t err, const char* what) {
@@ -713,7 +718,7 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
             r.status = Status(ErrorCode::kInvalidRequest, "prefill_chunk must be -1, 0 or positive", kComponent);
             return r;
         }
-        I.chunk_rows = want == -1 || !fits ? 0u : want == 0 ? 256u : uint32_t(want);
+        I.chunk_rows = want == -1 || !fits ? 0u : want == 0 ? kDefaultChunkRows : uint32_t(want);
         if (I.chunk_rows) {
             const size_t C = I.chunk_rows, rows = size_t(c.num_heads + 2 * c.num_kv_heads) * c.head_dim;
             LOAD_OR_RETURN(I.pf_x.Alloc(C * H * 4, false));

@@ -50,7 +50,7 @@ struct HipModelOptions {
     // 0 = as many as fit, -1 = none, n > 0 = at most n.
     int lds_prefetch = 0;
     // Prompt rows per prefill chunk pass (GEMMs on the matrix cores, causal
-    // chunk attention): 0 = 256, -1 = none (every prompt token through the
+    // chunk attention): 0 = 2048, -1 = none (every prompt token through the
     // fused decode step), n > 0 = n rows.
     int prefill_chunk = 0;
 };

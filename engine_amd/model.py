@@ -68,7 +68,7 @@ class Options:
     attn_max_splits: int = 0
     tile_rows: tuple = (0, 0, 0, 0, 0)   # qkv, o, gate/up, down, head; 0: device choice
     lds_prefetch: int = 0   # gate/up chunks per wave staged in LDS: 0 as many as fit, -1 none
-    prefill_chunk: int = 0  # prompt rows per chunk pass: 0 = 256, -1 = token by token (fused step)
+    prefill_chunk: int = 0  # prompt rows per chunk pass: 0 = 2048, -1 = token by token (fused step)
 
     def c(self):
         return L.ModelOptions(self.device_id, self.kv_pool_tokens, self.kv_block_tokens,

@@ -47,7 +47,7 @@ typedef struct lyk_model_options {
     /* gate/up chunks per wave staged in LDS during attention: 0 = as many
      * as fit (the default), -1 = none, n > 0 = at most n */
     int32_t lds_prefetch;
-    /* prompt rows per prefill chunk pass on the matrix cores: 0 = 256 (the
+    /* prompt rows per prefill chunk pass on the matrix cores: 0 = 2048 (the
      * default), -1 = none (every prompt token through the fused decode step),
      * n > 0 = n rows */
     int32_t prefill_chunk;

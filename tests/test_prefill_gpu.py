@@ -168,10 +168,11 @@ def _prefill_and_follow(hip, prompt, follow):
 @pytest.mark.parametrize("cfg", [MID, MID128], ids=["hd64", "hd128"])
 @pytest.mark.parametrize("mode", ["int4", "int8"])
 def test_chunked_prefill_matches_token_by_token(cuda, cfg, mode):
-    """Prompts of 2, 17 and 300 tokens (300: two chunks of 256 and one of
-    43): chunk sizes 256, 16 and 37 give bit-identical logits, before and
-    after 6 Decode steps; each within CHUNK_TOL of the token-by-token
-    Prefill, greedy tokens equal where the top-2 gap is not a tie."""
+    """Prompts of 2, 17 and 300 tokens: chunk sizes 2048 (the default, one
+    pass), 16 and 37 (many passes, the last one short) give bit-identical
+    logits, before and after 6 Decode steps; each within CHUNK_TOL of the
+    token-by-token Prefill, greedy tokens equal where the top-2 gap is not a
+    tie."""
     runs = {}
     for chunk in (0, 16, 37, -1):
         hip = M.HipModel.synthetic(cfg, seed=5, sigma=0.02, options=M.Options(quant=mode, prefill_chunk=chunk))
