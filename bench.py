@@ -34,6 +34,14 @@ times the isolated INT4 GEMV kernel (gemv.hip) at the four Qwen2.5-7B shapes
 of BASELINE config 2, M = 1, 2, 4, rotating over >= 512 MB of weight copies
 (2x the 256 MB MALL) so that every call reads HBM; one JSON line.
 
+  python bench.py --rows 4 [--model 7b|14b] [--quant int4|int8]
+BASELINE config 4's max_sequences=4 leg (config 5's decode leg with --model
+14b --quant int8 --prompts 256,1024,2048,4096): R sequences prefilled with
+their prompts, then K DecodeBatch steps of all R rows (logits to the host,
+greedy picks on the host, as a DecodeBatch caller does); one JSON line with
+aggregate tokens/s, the step kernel's time per launch from HIP events, and
+each prompt's time to first token.
+
   python bench.py --copy-calibration
 copies 1 GiB device to device 4 times (the runtime's plain copy kernel): the
 known-size reference that bench_profile.py scales the HBM counters by.
@@ -309,6 +317,60 @@ def cpu_baseline(context, tokens=3):
                         f"{t_token:.2f}s per token at context {context}"))
 
 
+def batch_bench(args):
+    """DecodeBatch throughput of R rows (config 4 / config 5 decode legs)."""
+    import torch
+    from engine_amd import model as M
+    cfg = M.QWEN25_7B if args.model == "7b" else M.QWEN25_14B
+    prompts = [int(p) for p in args.prompts.split(",")] if args.prompts else [args.prompt] * args.rows
+    assert len(prompts) == args.rows and 1 <= args.rows <= 4
+    pool = sum(prompts) + args.rows * (args.warmup + args.steps + 64)
+    t0 = time.time()
+    hip = M.HipModel.synthetic(cfg, seed=0, sigma=0.02, options=M.Options(quant=args.quant, kv_pool_tokens=pool))
+    log(f"[batch] load (synthetic {args.model}, {args.quant}) {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(1)
+    seqs, toks, ttft = [], [], []
+    warm = hip.new_seq(64)
+    assert hip.prefill(warm, list(range(1, 41)))[0] == 0
+    warm.close()
+    for n in prompts:
+        s = hip.new_seq(n + args.warmup + args.steps + 8)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        code, logits = hip.prefill(s, rng.integers(0, cfg.vocab_size, n).astype(np.uint32))
+        torch.cuda.synchronize()
+        ttft.append(round((time.perf_counter() - t1) * 1e3, 1))
+        assert code == 0
+        seqs.append(s)
+        toks.append(int(np.argmax(logits)))
+
+    def steps(k):
+        nonlocal toks
+        for _ in range(k):
+            code, per, out = hip.decode_batch(seqs, toks)
+            assert code == 0 and per == [0] * len(seqs)
+            toks = [int(v) for v in np.argmax(out, axis=1)]
+
+    steps(args.warmup)
+    stream = torch.cuda.ExternalStream(hip.stream_ptr)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    e0.record(stream)
+    steps(args.steps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t1
+    stream_us = e0.elapsed_time(e1) * 1e3 / args.steps
+    hip.close()
+    line = {"metric": f"DecodeBatch tok/s, {args.rows} sequences, Qwen2.5-{args.model.upper()} {args.quant.upper()} on 1 MI355X",
+            "value": round(args.rows * args.steps / dt, 2), "unit": "tok/s", "rows": args.rows,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / args.steps, 4),
+            "stream_us_per_step": round(stream_us, 1), "prompts": prompts, "ttft_ms": ttft,
+            "note": "each step: one fused-step launch for all rows, logits copied to the host, greedy on the host"}
+    print(json.dumps(line), flush=True)
+
+
 def gemv_bench(quant):
     """Isolated GEMV (gemv.hip, lyk_hip_gemv_q4/q8) at BASELINE config 2's
     Qwen2.5-7B shapes, M = 1, 2, 4, fp16 N(0, 1) activations, weights N(0,
@@ -434,6 +496,9 @@ def main():
     ap.add_argument("--prefill-gemm", action="store_true", help="time the prefill GEMM instead (one JSON line)")
     ap.add_argument("--sample", action="store_true", help="time device sampling instead (one JSON line)")
     ap.add_argument("--gemv", action="store_true", help="time the isolated GEMV at config 2 instead (one JSON line)")
+    ap.add_argument("--rows", type=int, default=1, help="DecodeBatch rows (>1: the batch leg instead, one JSON line)")
+    ap.add_argument("--model", choices=["7b", "14b"], default="7b", help="architecture of the --rows leg")
+    ap.add_argument("--prompts", default="", help="comma-separated prompt lengths of the --rows leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -453,6 +518,9 @@ def main():
         return
     if args.gemv:
         gemv_bench(args.quant)
+        return
+    if args.rows > 1:
+        batch_bench(args)
         return
     dec = run_decode(args)
     achieved = dec["step_bytes"] / (dec["kernel_us"] * 1e-6) / 1e9

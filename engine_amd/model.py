@@ -49,6 +49,8 @@ class QwenConfig:
 # Qwen2.5-7B (config.json of the released checkpoint): 28 layers, 28 query and
 # 4 KV heads of 128, SwiGLU 18944, vocab 152064, untied LM head.
 QWEN25_7B = QwenConfig(152064, 3584, 28, 28, 4, 128, 18944, 32768, 1e-6, 1e6, False, 151643)
+# Qwen2.5-14B: 48 layers, 40 query and 8 KV heads of 128, SwiGLU 13824.
+QWEN25_14B = QwenConfig(152064, 5120, 48, 40, 8, 128, 13824, 32768, 1e-6, 1e6, False, 151643)
 
 
 def _config(cfg):
