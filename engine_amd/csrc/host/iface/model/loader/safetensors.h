@@ -13,7 +13,9 @@
 
 namespace lykuro::nie {
 
-enum class Dtype { kBf16, kF16, kF32 };
+// kU8 / kI8 extend the reference's allowlist (safetensors.h:21) for
+// offline-quantized artifacts: packed int4 codes (U8) and int8 codes (I8).
+enum class Dtype { kBf16, kF16, kF32, kU8, kI8 };
 
 size_t DtypeSize(Dtype dtype);
 std::string_view DtypeName(Dtype dtype);

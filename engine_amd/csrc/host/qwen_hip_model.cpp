@@ -211,7 +211,49 @@ Status SafetensorsWeightSource::Read(const std::string& name, const std::vector<
         case Dtype::kBf16:
             for (uint64_t i = 0; i < info->element_count; ++i) out[i] = lyk::bf16_to_f32(h[i]);
             break;
+        default:
+            return Status(ErrorCode::kArtifactVerificationFailed, "weight tensor is not floating point", kComponent);
     }
+    return Status::Ok();
+}
+
+Status SafetensorsWeightSource::ReadQuantized(const std::string& base, bool q8, int64_t n, int64_t k,
+                                              std::vector<int8_t>& codes, std::vector<uint16_t>& scales,
+                                              bool& found) const {
+    found = false;
+    const TensorInfo* w = file_.FindTensor(base + ".qweight");
+    const TensorInfo* s = file_.FindTensor(base + ".qscale");
+    if (w == nullptr && s == nullptr) return Status::Ok();
+    if (w == nullptr || s == nullptr)
+        return Status(ErrorCode::kArtifactVerificationFailed, "quantized weight without its scales", kComponent);
+    // int4: U8 [n][ceil(k/2)], code + 8 per nibble, even k in the low nibble,
+    // fp16 scales [n][ceil(k/32)]; int8: I8 [n][k], fp16 scales [n]
+    const bool is_q8 = w->dtype == Dtype::kI8;
+    if ((w->dtype != Dtype::kU8 && w->dtype != Dtype::kI8) || s->dtype != Dtype::kF16)
+        return Status(ErrorCode::kArtifactVerificationFailed, "quantized weight dtypes invalid", kComponent);
+    if (is_q8 != q8)
+        return Status(ErrorCode::kUnsupportedModel, "artifact quantization differs from the model options", kComponent);
+    const std::vector<uint64_t> wshape = {uint64_t(n), uint64_t(q8 ? k : (k + 1) / 2)};
+    const std::vector<uint64_t> sshape = q8 ? std::vector<uint64_t>{uint64_t(n)}
+                                            : std::vector<uint64_t>{uint64_t(n), uint64_t((k + 31) / 32)};
+    if (w->shape != wshape || s->shape != sshape)
+        return Status(ErrorCode::kArtifactVerificationFailed, "quantized weight shape mismatch", kComponent);
+    const uint8_t* wd = file_.TensorData(base + ".qweight");
+    const uint8_t* sd = file_.TensorData(base + ".qscale");
+    codes.resize(size_t(n * k));
+    scales.resize(s->element_count);
+    std::memcpy(scales.data(), sd, s->data_size);
+    if (q8) {
+        std::memcpy(codes.data(), wd, size_t(n * k));
+    } else {
+        const int64_t kb = (k + 1) / 2;
+        for (int64_t r = 0; r < n; ++r)
+            for (int64_t i = 0; i < k; ++i) {
+                const uint8_t byte = wd[r * kb + i / 2];
+                codes[size_t(r * k + i)] = int8_t(int((i & 1) ? byte >> 4 : byte & 15) - 8);
+            }
+    }
+    found = true;
     return Status::Ok();
 }
 
@@ -478,34 +520,38 @@ struct QwenHipModel::Impl {
 
 namespace {
 
-Status QuantizeUpload(bool q8, const std::vector<float>& a, const std::vector<float>* b, int64_t n,
-                      int64_t k, bool normed_input, int tile_rows, PackedMat& out, uint64_t& bytes) {
-    const int64_t ns = q8 ? 1 : (k + 31) / 32;
-    std::vector<int8_t> ca((size_t)(n * k)), cb;
-    std::vector<uint16_t> sa((size_t)(n * ns)), sb;
-    int rc = q8 ? lyk_q8_quantize(a.data(), n, k, ca.data(), sa.data())
-                : lyk_q4_quantize(a.data(), n, k, ca.data(), sa.data());
+// Codes and fp16 scales of an [n, k] fp32 matrix by the load-time quantizer
+// (int4: groups of 32 along k; int8: per row).
+Status Quantize(bool q8, const std::vector<float>& w, int64_t n, int64_t k, std::vector<int8_t>& codes,
+                std::vector<uint16_t>& scales) {
+    codes.resize(size_t(n * k));
+    scales.resize(size_t(n * (q8 ? 1 : (k + 31) / 32)));
+    const int rc = q8 ? lyk_q8_quantize(w.data(), n, k, codes.data(), scales.data())
+                      : lyk_q4_quantize(w.data(), n, k, codes.data(), scales.data());
     if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight quantization failed", kComponent);
-    if (b) {
-        cb.resize(ca.size());
-        sb.resize(sa.size());
-        rc = q8 ? lyk_q8_quantize(b->data(), n, k, cb.data(), sb.data())
-                : lyk_q4_quantize(b->data(), n, k, cb.data(), sb.data());
-        if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight quantization failed", kComponent);
-    }
+    return Status::Ok();
+}
+
+// Packs codes and scales (paired: b beside a, gate and up) into the fused
+// step's tiled layout and uploads them.
+Status PackUpload(bool q8, const std::vector<int8_t>& ca, const std::vector<uint16_t>& sa,
+                  const std::vector<int8_t>* cbp, const std::vector<uint16_t>* sbp, int64_t n, int64_t k,
+                  bool normed_input, int tile_rows, PackedMat& out, uint64_t& bytes) {
+    const bool paired = cbp != nullptr;
+    int rc;
     // the tile height the fused step streams this shape best with on this device
-    const int tr = tile_rows ? tile_rows : lyk_hip_step_tile_rows(n, k, b != nullptr, q8 ? 1 : 0, normed_input ? 1 : 0);
+    const int tr = tile_rows ? tile_rows : lyk_hip_step_tile_rows(n, k, paired, q8 ? 1 : 0, normed_input ? 1 : 0);
     if (tr == 0) return Status(ErrorCode::kGpuUnhealthy, "hip device properties unavailable", kComponent);
     if (tr != 16 && tr != 32 && tr != 64) return Status(ErrorCode::kUnsupportedModel, "tile height must be 16, 32 or 64", kComponent);
     uint64_t wb = 0, sbytes = 0;
-    rc = q8 ? lyk_q8_layout_tiled(n, k, b != nullptr, tr, &wb, &sbytes)
-            : lyk_q4_layout_tiled(n, k, b != nullptr, tr, &wb, &sbytes);
+    rc = q8 ? lyk_q8_layout_tiled(n, k, paired, tr, &wb, &sbytes)
+            : lyk_q4_layout_tiled(n, k, paired, tr, &wb, &sbytes);
     if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight shape unsupported", kComponent);
     std::vector<uint8_t> qw(wb), qs(sbytes);
-    rc = q8 ? lyk_q8_pack_tiled(ca.data(), sa.data(), b ? cb.data() : nullptr, b ? sb.data() : nullptr, n, k, tr,
-                                qw.data(), qs.data())
-            : lyk_q4_pack_tiled(ca.data(), sa.data(), b ? cb.data() : nullptr, b ? sb.data() : nullptr, n, k, tr,
-                                qw.data(), qs.data());
+    const int8_t* cb = paired ? cbp->data() : nullptr;
+    const uint16_t* sb = paired ? sbp->data() : nullptr;
+    rc = q8 ? lyk_q8_pack_tiled(ca.data(), sa.data(), cb, sb, n, k, tr, qw.data(), qs.data())
+            : lyk_q4_pack_tiled(ca.data(), sa.data(), cb, sb, n, k, tr, qw.data(), qs.data());
     if (rc != LYK_OK) return Status(ErrorCode::kUnsupportedModel, "weight packing failed", kComponent);
     Status s = out.qw.Upload(qw.data(), qw.size());
     if (!s.ok()) return s;
@@ -513,10 +559,10 @@ Status QuantizeUpload(bool q8, const std::vector<float>& a, const std::vector<fl
     if (!s.ok()) return s;
     out.n = n;
     out.k = k;
-    out.paired = b != nullptr;
+    out.paired = paired;
     out.tile_rows = tr;
     // bytes a step reads: codes and scales of the real rows (no tile padding)
-    const int64_t rows = n * (b ? 2 : 1);
+    const int64_t rows = n * (paired ? 2 : 1);
     bytes += q8 ? uint64_t(rows * k + rows * 2) : uint64_t(rows * ((k + 1) / 2) + rows * ((k + 31) / 32) * 2);
     return Status::Ok();
 }
@@ -575,6 +621,24 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
         ++expected;
         return src.Read(name, shape, out);
     };
+    // An [n, k] GEMV matrix as codes and scales: offline-quantized in the
+    // source (`base`.qweight / .qscale), else `base`.weight quantized here.
+    auto codes_of = [&](const std::string& base, uint64_t n, uint64_t k, std::vector<int8_t>& codes,
+                        std::vector<uint16_t>& scales) -> Status {
+        bool found = false;
+        Status s = src.ReadQuantized(base, I.q8, int64_t(n), int64_t(k), codes, scales, found);
+        if (!s.ok()) return s;
+        if (found) {
+            expected += 2;
+            return Status::Ok();
+        }
+        std::vector<float> w;
+        s = read(base + ".weight", {n, k}, w);
+        if (!s.ok()) return s;
+        return Quantize(I.q8, w, int64_t(n), int64_t(k), codes, scales);
+    };
+    std::vector<int8_t> ca, cb, ct;
+    std::vector<uint16_t> sa, sb, st;
 #define LOAD_OR_RETURN(expr)         \
     do {                             \
         Status s_ = (expr);          \
@@ -594,36 +658,48 @@ QwenHipModel::LoadResult QwenHipModel::Load(const ModelManifest& manifest, const
         LOAD_OR_RETURN(UploadF32(a, L.input_norm));
         LOAD_OR_RETURN(read(LayerName(l, "post_attention_layernorm.weight"), {H}, a));
         LOAD_OR_RETURN(UploadF32(a, L.post_norm));
-        // fused qkv: rows [q | k | v], bias concatenated the same way
-        std::vector<float> qkv, bias, t;
-        LOAD_OR_RETURN(read(LayerName(l, "self_attn.q_proj.weight"), {qd, H}, t));
-        qkv.insert(qkv.end(), t.begin(), t.end());
-        LOAD_OR_RETURN(read(LayerName(l, "self_attn.k_proj.weight"), {kvd, H}, t));
-        qkv.insert(qkv.end(), t.begin(), t.end());
-        LOAD_OR_RETURN(read(LayerName(l, "self_attn.v_proj.weight"), {kvd, H}, t));
-        qkv.insert(qkv.end(), t.begin(), t.end());
+        // fused qkv: rows [q | k | v] (codes and per-row scales
+        // concatenated), bias concatenated the same way
+        std::vector<float> bias, t;
+        ca.clear();
+        sa.clear();
+        for (const char* nm : {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"}) {
+            LOAD_OR_RETURN(codes_of(LayerName(l, nm), std::string(nm) == "self_attn.q_proj" ? qd : kvd, H, ct, st));
+            ca.insert(ca.end(), ct.begin(), ct.end());
+            sa.insert(sa.end(), st.begin(), st.end());
+        }
         for (const char* nm : {"self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias"}) {
             LOAD_OR_RETURN(read(LayerName(l, nm), {std::string(nm).find("q_proj") != std::string::npos ? qd : kvd}, t));
             bias.insert(bias.end(), t.begin(), t.end());
         }
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, qkv, nullptr, int64_t(qd + 2 * kvd), int64_t(H), true, options.tile_rows[0], L.qkv, I.gemv_bytes));
+        LOAD_OR_RETURN(PackUpload(I.q8, ca, sa, nullptr, nullptr, int64_t(qd + 2 * kvd), int64_t(H), true,
+                                  options.tile_rows[0], L.qkv, I.gemv_bytes));
         LOAD_OR_RETURN(UploadF32(bias, L.qkv_bias));
-        LOAD_OR_RETURN(read(LayerName(l, "self_attn.o_proj.weight"), {H, qd}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(qd), false, options.tile_rows[1], L.o, I.gemv_bytes));
-        LOAD_OR_RETURN(read(LayerName(l, "mlp.gate_proj.weight"), {In, H}, a));
-        LOAD_OR_RETURN(read(LayerName(l, "mlp.up_proj.weight"), {In, H}, b));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, &b, int64_t(In), int64_t(H), true, options.tile_rows[2], L.gateup, I.gemv_bytes));
-        LOAD_OR_RETURN(read(LayerName(l, "mlp.down_proj.weight"), {H, In}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(H), int64_t(In), false, options.tile_rows[3], L.down, I.gemv_bytes));
+        LOAD_OR_RETURN(codes_of(LayerName(l, "self_attn.o_proj"), H, qd, ca, sa));
+        LOAD_OR_RETURN(PackUpload(I.q8, ca, sa, nullptr, nullptr, int64_t(H), int64_t(qd), false, options.tile_rows[1],
+                                  L.o, I.gemv_bytes));
+        LOAD_OR_RETURN(codes_of(LayerName(l, "mlp.gate_proj"), In, H, ca, sa));
+        LOAD_OR_RETURN(codes_of(LayerName(l, "mlp.up_proj"), In, H, cb, sb));
+        LOAD_OR_RETURN(PackUpload(I.q8, ca, sa, &cb, &sb, int64_t(In), int64_t(H), true, options.tile_rows[2],
+                                  L.gateup, I.gemv_bytes));
+        LOAD_OR_RETURN(codes_of(LayerName(l, "mlp.down_proj"), H, In, ca, sa));
+        LOAD_OR_RETURN(PackUpload(I.q8, ca, sa, nullptr, nullptr, int64_t(H), int64_t(In), false, options.tile_rows[3],
+                                  L.down, I.gemv_bytes));
     }
     LOAD_OR_RETURN(read("model.norm.weight", {H}, a));
     LOAD_OR_RETURN(UploadF32(a, I.final_norm));
     if (c.tie_word_embeddings) {
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, embed, nullptr, int64_t(V), int64_t(H), true, options.tile_rows[4], I.lm_head, I.gemv_bytes));
+        // the head is the embedding; an offline-quantized artifact may carry
+        // its quantized form as lm_head.qweight / .qscale
+        bool found = false;
+        LOAD_OR_RETURN(src.ReadQuantized("lm_head", I.q8, int64_t(V), int64_t(H), ca, sa, found));
+        if (found) expected += 2;
+        else LOAD_OR_RETURN(Quantize(I.q8, embed, int64_t(V), int64_t(H), ca, sa));
     } else {
-        LOAD_OR_RETURN(read("lm_head.weight", {V, H}, a));
-        LOAD_OR_RETURN(QuantizeUpload(I.q8, a, nullptr, int64_t(V), int64_t(H), true, options.tile_rows[4], I.lm_head, I.gemv_bytes));
+        LOAD_OR_RETURN(codes_of("lm_head", V, H, ca, sa));
     }
+    LOAD_OR_RETURN(PackUpload(I.q8, ca, sa, nullptr, nullptr, int64_t(V), int64_t(H), true, options.tile_rows[4],
+                              I.lm_head, I.gemv_bytes));
     if (src.tensor_count() != expected) {
         r.status = Status(ErrorCode::kArtifactVerificationFailed, "weight file contains unexpected tensors",
                           kComponent);

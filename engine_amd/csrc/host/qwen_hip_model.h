@@ -66,6 +66,15 @@ public:
                         std::vector<float>& out) const = 0;
     // Number of tensors the source holds (the loader rejects extras).
     virtual size_t tensor_count() const = 0;
+    // An offline-quantized [n, k] matrix stored as `base`.qweight and
+    // `base`.qscale (the loader's own codes and fp16 scales: int4 groups of
+    // 32, int8 per row); found = false when the source holds none.
+    virtual Status ReadQuantized(const std::string& base, bool q8, int64_t n, int64_t k,
+                                 std::vector<int8_t>& codes, std::vector<uint16_t>& scales, bool& found) const {
+        (void)base, (void)q8, (void)n, (void)k, (void)codes, (void)scales;
+        found = false;
+        return Status::Ok();
+    }
 };
 
 // A safetensors file as a weight source (F32 / F16 / BF16, widened to fp32
@@ -76,6 +85,8 @@ public:
     Status Read(const std::string& name, const std::vector<uint64_t>& shape,
                 std::vector<float>& out) const override;
     size_t tensor_count() const override { return file_.header().tensors.size(); }
+    Status ReadQuantized(const std::string& base, bool q8, int64_t n, int64_t k, std::vector<int8_t>& codes,
+                         std::vector<uint16_t>& scales, bool& found) const override;
 
 private:
     const SafetensorsFile& file_;

@@ -135,19 +135,30 @@ bool ParseDtype(const std::string& s, Dtype& d) {
     if (s == "BF16") d = Dtype::kBf16;
     else if (s == "F16") d = Dtype::kF16;
     else if (s == "F32") d = Dtype::kF32;
+    else if (s == "U8") d = Dtype::kU8;
+    else if (s == "I8") d = Dtype::kI8;
     else return false;
     return true;
 }
 
 }  // namespace
 
-size_t DtypeSize(Dtype dtype) { return dtype == Dtype::kF32 ? 4 : 2; }
+size_t DtypeSize(Dtype dtype) {
+    switch (dtype) {
+        case Dtype::kF32: return 4;
+        case Dtype::kU8:
+        case Dtype::kI8: return 1;
+        default: return 2;
+    }
+}
 
 std::string_view DtypeName(Dtype dtype) {
     switch (dtype) {
         case Dtype::kBf16: return "BF16";
         case Dtype::kF16: return "F16";
         case Dtype::kF32: return "F32";
+        case Dtype::kU8: return "U8";
+        case Dtype::kI8: return "I8";
     }
     return "?";
 }
