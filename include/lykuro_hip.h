@@ -300,7 +300,7 @@ int lyk_hip_sample(const float* d_logits, int64_t ldl, int m, int64_t n,
 /* lyk_hip_sample without a caller workspace, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference. The
- * scratch is a file-scope device array of 16 MiB (4 rows of up to 2^18
+ * scratch is a file-scope device array of 24 MiB (4 rows of up to 2^18
  * logits), one per GPU the library runs on, held until the process ends;
  * n > 2^18 returns LYK_ERR_SHAPE. Nothing is allocated or freed. Calls that
  * overlap in time on one GPU (different streams, no ordering between them)

@@ -118,18 +118,23 @@ def test_sample_reference_cases(cuda, golden):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n", [1000, 152064])
 @pytest.mark.parametrize("bad", [float("inf"), float("-inf"), float("nan")])
-def test_sample_non_finite_fails_the_row(cuda, bad):
-    x = logits_of("normal", 1000, 3)
-    x[500] = bad
+def test_sample_non_finite_fails_the_row(cuda, bad, n):
+    """Both paths: one launch (n = 1000) and the wide rows' prep / sort /
+    finish (n = 152064 without top_k)."""
+    x = logits_of("normal", n, 3)
+    x[n // 2] = bad
     assert device_tokens(x, 0.8, 0, 0.9, 1, 1) == [-1]
     assert device_tokens(x, 0.0, 0, 1.0, 1, 1) == [-1]
 
 
 @pytest.mark.gpu
-def test_sample_rows_are_independent(cuda):
-    """Four rows in one launch give each row's single-row token."""
-    rows = np.stack([logits_of(kind, 5000, i) for i, kind in enumerate(["normal", "peaked", "ties", "normal"])])
+@pytest.mark.parametrize("n", [5000, 40000])
+def test_sample_rows_are_independent(cuda, n):
+    """Four rows in one call give each row's single-row token (n = 40000:
+    the wide rows' path)."""
+    rows = np.stack([logits_of(kind, n, i) for i, kind in enumerate(["normal", "peaked", "ties", "normal"])])
     x = torch.from_numpy(rows).cuda()
     u = [0.1, 0.5, 0.9, 0.999]
     got = ops.sample(x, 0.9, 0, 0.95, u).cpu().tolist()
