@@ -117,10 +117,13 @@ __device__ __forceinline__ bool take(const u64* p, uint32_t tag, uint32_t& paylo
 __device__ __forceinline__ uint32_t fbits(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ float bitsf(uint32_t u) { return __builtin_bit_cast(float, u); }
 
-// One attempt at N tagged words. All N loads are issued, unconditionally,
-// before any is tested, so an attempt costs one memory round trip for the
-// whole batch (testing a word before the next load is issued costs a round
-// trip per word). at(u) must give a readable address for every u; word u is
+// One attempt at N tagged words. The loads of every word still missing are
+// issued before any is tested, so an attempt costs one memory round trip for
+// the whole batch (testing a word before the next load is issued costs a
+// round trip per word); words already in are not read again. (Polling one
+// word until something arrives, then the rest, was measured slower: the
+// extra round trip lands on the late workgroups.) at(u) must give a readable
+// address for every u; word u is
 // wanted when bit u of `want` is set and it has not arrived yet (bit u of
 // `have`), and got(u, payload) takes it on arrival. Returns the wanted
 // words still missing.
@@ -130,7 +133,7 @@ __device__ __forceinline__ int poll_batch(uint32_t want, uint32_t& have, uint32_
     const uint32_t pend = want & ~have;
     u64 w[N];
 #pragma unroll
-    for (int u = 0; u < N; ++u) w[u] = load_sc1(at(u));
+    for (int u = 0; u < N; ++u) w[u] = (pend >> u & 1) ? load_sc1(at(u)) : 0ull;
     int missing = 0;
 #pragma unroll
     for (int u = 0; u < N; ++u) {
@@ -616,11 +619,11 @@ struct WindowIn {
 __device__ __forceinline__ void load_gamma(const StepArgs& a, const float* gamma, const Mat& A, const Part& p,
                                            int tid, float (&g)[kNormPer]) {
     const int H = a.md.hidden_size;
+    const int lo = p.ca * A.ck, hi = (p.ca + p.win) * A.ck;   // the window's k range
 #pragma unroll
     for (int j = 0; j < kNormPer; ++j) {
         const int i = tid + j * kThreads;
-        const int slot = i / A.ck - p.ca;
-        g[j] = p.busy && i < H && slot >= 0 && slot < p.win ? ld(gamma + i) : 0.0f;
+        g[j] = p.busy && i < H && i >= lo && i < hi ? ld(gamma + i) : 0.0f;
     }
 }
 
@@ -644,25 +647,20 @@ __device__ __forceinline__ void norm_window(const StepArgs& a, const float (&h)[
     float scale[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) scale[m] = 1.0f / sqrtf(ss[m] / (float)H + a.md.rms_norm_eps);
+    // window slot s holds chunk ca + s, so k index i sits at i - lo
+    const int lo = p.ca * CK, hi = (p.ca + p.win) * CK, xstride = p.win * CK;
 #pragma unroll
     for (int j = 0; j < kNormPer; ++j) {
         const int i = tid + j * kThreads;
-        if (i < H) {
-            const int slot = i / CK - p.ca;
-            if (slot >= 0 && slot < p.win) {
-                const float g = gv[j];
+        if (i < H && i >= lo && i < hi) {
+            const float g = gv[j];
 #pragma unroll
-                for (int m = 0; m < M; ++m)
-                    xs[((size_t)m * p.win + slot) * CK + (i % CK)] = f2h(h[m][j] * scale[m] * g);
-            }
+            for (int m = 0; m < M; ++m) xs[(size_t)m * xstride + (i - lo)] = f2h(h[m][j] * scale[m] * g);
         }
     }
-    const int kp = (p.ca + p.win) * CK;
-    for (int i = (H > p.ca * CK ? H : p.ca * CK) + tid; i < kp; i += kThreads) {
-        const int slot = i / CK - p.ca;
+    for (int i = (H > lo ? H : lo) + tid; i < hi; i += kThreads)
 #pragma unroll
-        for (int m = 0; m < M; ++m) xs[((size_t)m * p.win + slot) * CK + (i % CK)] = 0;
-    }
+        for (int m = 0; m < M; ++m) xs[(size_t)m * xstride + (i - lo)] = 0;
 }
 
 struct Best {
@@ -854,7 +852,12 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                     if (!end) srow = h2f(ld(static_cast<const uint16_t*>(A.s) + (size_t)t * 64 + lane));
             }
             if (end) return true;
-            if (refill && f + 2 < w1) CM::load(A, f + 2, nv_of(f + 2), lane, wbuf, sbuf);
+            if (refill && f + 2 < w1) {
+                // chunk f + 2's place in its tile, from c (no division)
+                int c2 = c + 2;
+                while (c2 >= A.chunks) c2 -= A.chunks;
+                CM::load(A, f + 2, tail == kChunkBlocks || c2 + 1 < A.chunks ? kChunkBlocks : tail, lane, wbuf, sbuf);
+            }
             __builtin_amdgcn_sched_barrier(0);
             ++f;
             c = c + 1 == A.chunks ? 0 : c + 1;
@@ -864,7 +867,8 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
         for (int i = 0; i < npf && !done; ++i) {
             u32x4 wl[kChunkBlocks];
             u64 sl = 0;
-            CM::load_lds(pfb + i * kSlotBytes<Q8>, nv_of(f), lane, wl, sl);
+            CM::load_lds(pfb + i * kSlotBytes<Q8>, tail == kChunkBlocks || c + 1 < A.chunks ? kChunkBlocks : tail,
+                         lane, wl, sl);
             done = step(wl, sl, false);
         }
         while (!done) {
@@ -1091,6 +1095,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
     mark(a, ph, 0);
     const int nq = a.md.num_heads, nkv = a.md.num_kv_heads;
     const int G = nq / nkv, bt = a.md.block_tokens;
+    const int bt_log = (bt & (bt - 1)) == 0 ? __builtin_ctz(bt) : -1;   // block lookups by shift
     const int lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, quad = lane >> 4;   // MFMA column / row quad of this lane
     const float scale = 1.0f / sqrtf((float)HD);
@@ -1157,7 +1162,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         u32x4 kr[kKTiles][KS];
         u64 vr[kChunkTiles];
         auto tile_block = [&](int tt, int& slot) -> size_t {   // tt: first token of a tile
-            const int tb = uniform(tt) / bt;
+            const int tb = bt_log >= 0 ? uniform(tt) >> bt_log : uniform(tt) / bt;
             slot = uniform(tt) - tb * bt;
             return (size_t)ld(tab + tb) * blk_stride;
         };
@@ -1441,11 +1446,14 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 return a.attn_acc + (grp * kAttnMaxSplits + k % Sm) * (size_t)GH + e0 + k / Sm;
             };
             uint32_t want = 0, have = 0;
+            const u64* at[4];   // the words' addresses, once for every attempt
 #pragma unroll
-            for (int u2 = 0; u2 < 4; ++u2)
+            for (int u2 = 0; u2 < 4; ++u2) {
                 if (b0 + u2 * kThreads < nw) want |= 1u << u2;
+                at[u2] = word(min(b0 + u2 * kThreads, nw - 1));
+            }
             auto pending = [&]() {
-                return poll_batch<4>(want, have, tag, [&](int u2) { return word(min(b0 + u2 * kThreads, nw - 1)); },
+                return poll_batch<4>(want, have, tag, [&](int u2) { return at[u2]; },
                                      [&](int u2, uint32_t x) { v[u2] = x; });
             };
             ok = spin(a, pending) && ok;
