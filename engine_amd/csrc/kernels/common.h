@@ -73,6 +73,64 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Lane pairs (l, l ^ 32) and (l, l ^ 16) combined through the gfx950
+// permlane swaps: each lane receives both values of its pair in VGPRs, with
+// no LDS round trip (a shuffle goes through ds_bpermute and waits for it).
+// The combination is commutative, so both lanes of a pair get the same bits,
+// the bits a shuffle exchange gives. Every lane of the wave must be active.
+// Both swap operands start as v; the compiler folds the swap of one value
+// with itself into two equal results (the hardware gives the two rows of
+// each pair), so the copy and the results pass through empty asm it cannot
+// see through.
+template <bool Row32>
+__device__ __forceinline__ void pair_of(float v, float& x, float& y) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    unsigned w;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(w) : "v"(u));
+    const auto r = Row32 ? __builtin_amdgcn_permlane32_swap(u, w, false, false)
+                         : __builtin_amdgcn_permlane16_swap(u, w, false, false);
+    unsigned a = r[0], b = r[1];
+    asm volatile("" : "+v"(a), "+v"(b));
+    x = __builtin_bit_cast(float, a);
+    y = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float pair32_sum(float v) {
+    float x, y;
+    pair_of<true>(v, x, y);
+    return x + y;
+}
+__device__ __forceinline__ float pair16_sum(float v) {
+    float x, y;
+    pair_of<false>(v, x, y);
+    return x + y;
+}
+__device__ __forceinline__ float pair32_max(float v) {
+    float x, y;
+    pair_of<true>(v, x, y);
+    return fmaxf(x, y);
+}
+__device__ __forceinline__ float pair16_max(float v) {
+    float x, y;
+    pair_of<false>(v, x, y);
+    return fmaxf(x, y);
+}
+// v + the value of the lane `CTRL` names within its 16-lane row (DPP).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// Sum over the wave without LDS: rotations by 8, 4, 2, 1 within each 16-lane
+// row (after each, the lanes a rotation pairs hold equal bits), then the
+// row pairs and halves through the permlane swaps. Every lane gets the same
+// bits; the order is fixed. Every lane of the wave must be active.
+__device__ __forceinline__ float wave_total(float v) {
+    v = dpp_add<0x128>(v);   // row_ror:8
+    v = dpp_add<0x124>(v);   // row_ror:4
+    v = dpp_add<0x122>(v);   // row_ror:2
+    v = dpp_add<0x121>(v);   // row_ror:1
+    return pair32_sum(pair16_sum(v));
+}
+
 // Global-memory view of a generic pointer. Pointers that reach a kernel
 // through a struct in device memory lose their address space; accesses
 // through them would compile to flat instructions, which also count against

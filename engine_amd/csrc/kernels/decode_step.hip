@@ -120,20 +120,21 @@ __device__ __forceinline__ float bitsf(uint32_t u) { return __builtin_bit_cast(f
 // One attempt at N tagged words. The loads of every word still missing are
 // issued before any is tested, so an attempt costs one memory round trip for
 // the whole batch (testing a word before the next load is issued costs a
-// round trip per word); words already in are not read again. (Polling one
+// round trip per word); words already in are not read again (Skip; the
+// multi-row kernels re-read them, which keeps their register budget). (Polling one
 // word until something arrives, then the rest, was measured slower: the
 // extra round trip lands on the late workgroups.) at(u) must give a readable
 // address for every u; word u is
 // wanted when bit u of `want` is set and it has not arrived yet (bit u of
 // `have`), and got(u, payload) takes it on arrival. Returns the wanted
 // words still missing.
-template <int N, class At, class Got>
+template <int N, bool Skip = true, class At, class Got>
 __device__ __forceinline__ int poll_batch(uint32_t want, uint32_t& have, uint32_t tag, At at, Got got) {
     static_assert(N <= 32, "batch");
     const uint32_t pend = want & ~have;
     u64 w[N];
 #pragma unroll
-    for (int u = 0; u < N; ++u) w[u] = (pend >> u & 1) ? load_sc1(at(u)) : 0ull;
+    for (int u = 0; u < N; ++u) w[u] = !Skip || (pend >> u & 1) ? load_sc1(at(u)) : 0ull;
     int missing = 0;
 #pragma unroll
     for (int u = 0; u < N; ++u) {
@@ -221,7 +222,7 @@ __device__ __forceinline__ void block_sum_rows(float (&v)[M], int tid) {
     const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        const float s = wave_sum(v[m]);
+        const float s = wave_total(v[m]);
         if (lane == 0) part[wave][m] = s;
     }
     __syncthreads();
@@ -554,7 +555,7 @@ struct ResidualIn {
         for (int q = 0; q < NB; ++q) {
             const int m0 = q * RB;
             const uint32_t wq = m0 + RB <= M ? want : want & 0x55555555u;   // last batch of odd M: one row
-            missing += poll_batch<kNormPer * RB>(
+            missing += poll_batch<kNormPer * RB, M == 1>(
                 wq, have[q], tag,
                 [&](int u) {
                     return d + (size_t)min(m0 + u % RB, M - 1) * H + min(tid + (u / RB) * kThreads, H - 1);
@@ -598,7 +599,7 @@ struct WindowIn {
         int missing = 0;
 #pragma unroll
         for (int m = 0; m < M; ++m)
-            missing += poll_batch<kWinWords>(want[m], have[m], tag,
+            missing += poll_batch<kWinWords, M == 1>(want[m], have[m], tag,
                                              [&](int u) { return src(m) + min(tid + u * kThreads, valid - 1); },
                                              [&](int u, uint32_t x) { v[m][u] = x; });
         return missing;
@@ -883,7 +884,10 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     for (int q = 0; q < kPieces; ++q)
 #pragma unroll
         for (int m = 0; m < M; ++m)
-            for (int o = A.tr; o < 64; o <<= 1) accq[q][m] += __shfl_xor(accq[q][m], o, 64);
+        {
+            if (A.tr <= 16) accq[q][m] = pair16_sum(accq[q][m]);
+            if (A.tr <= 32) accq[q][m] = pair32_sum(accq[q][m]);
+        }
     // each wave's tile sums, and the tiles [first, last] its range touched
     __shared__ int span[kWaves][2];
     {
@@ -951,7 +955,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                     const int m0 = q * RB, rb = m0 + RB <= M ? RB : M - m0;
                     uint32_t want = 0;
                     for (int s2 = 1; s2 < np; ++s2) want |= ((1u << rb) - 1) << ((s2 - 1) * RB);
-                    missing += poll_batch<(kMaxPieces - 1) * RB>(
+                    missing += poll_batch<(kMaxPieces - 1) * RB, M == 1>(
                         want, have[q], tag,
                         [&](int u) {
                             return part + ((size_t)min(u / RB, np - 2) * M + min(m0 + u % RB, M - 1)) * 64;
@@ -1335,8 +1339,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                     }
                 }
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = pair32_max(pair16_max(mx));
             if (lane < 16) wmax[wave][lane] = mx;
             if (c + 1 < nch) load_k(c0 + kChunkT);   // next chunk, in flight meanwhile
             __syncthreads();
@@ -1359,7 +1362,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                     for (int j = 0; j < 4; ++j)
                         if (tt + j < n) p[j] = expf(sc[h * SS + tt + j] - mh);
                 }
-                const float sum = wave_sum((p[0] + p[1]) + (p[2] + p[3]));
+                const float sum = wave_total((p[0] + p[1]) + (p[2] + p[3]));
                 uint16_t hi[4], lo[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) split_f16(p[j], hi[j], lo[j]);
@@ -1472,7 +1475,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
             const float ms = live ? mlv[(lane * G + h) * 2] : -INFINITY;
             const float mx = wave_max(ms);
             const float es = live ? expf(ms - mx) : 0.0f;
-            const float L = wave_sum(live ? mlv[(lane * G + h) * 2 + 1] * es : 0.0f);
+            const float L = wave_total(live ? mlv[(lane * G + h) * 2 + 1] * es : 0.0f);
             if (live) mlv[(lane * G + h) * 2] = es;
             if (lane == 0) lsum[h] = L;
         }
