@@ -672,6 +672,29 @@ __device__ __forceinline__ Best better(Best x, Best y) {
     if (y.v > x.v || (y.v == x.v && y.i < x.i)) return y;
     return x;
 }
+// The wave's best (largest value, then smallest index) in every lane, without
+// LDS: DPP rotations within each 16-lane row, then the permlane swaps. better
+// selects from a total order, so the combination order does not matter.
+template <int CTRL>
+__device__ __forceinline__ Best dpp_better(Best b) {
+    return better(b, Best{__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, b.v), CTRL,
+                                                                                 0xf, 0xf, false)),
+                          __builtin_amdgcn_update_dpp(0, b.i, CTRL, 0xf, 0xf, false)});
+}
+template <bool Row32>
+__device__ __forceinline__ Best pair_better(Best b) {
+    float xv, yv, xi, yi;
+    pair_of<Row32>(b.v, xv, yv);
+    pair_of<Row32>(__builtin_bit_cast(float, b.i), xi, yi);
+    return better(Best{xv, __builtin_bit_cast(int, xi)}, Best{yv, __builtin_bit_cast(int, yi)});
+}
+__device__ __forceinline__ Best wave_best(Best b) {
+    b = dpp_better<0x128>(b);   // row_ror:8
+    b = dpp_better<0x124>(b);   // row_ror:4
+    b = dpp_better<0x122>(b);   // row_ror:2
+    b = dpp_better<0x121>(b);   // row_ror:1
+    return pair_better<true>(pair_better<false>(b));
+}
 
 enum Kind { kQkv = 0, kAttn = 1, kOut = 2, kGateUp = 3, kDown = 4, kHead = 5 };
 
@@ -1000,10 +1023,17 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                 const int j = t * half + lane;
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    const float up = __shfl_down(v[m], half, 64);
+                    // lane + half's value (the up row) and lane + 1's act, in
+                    // VGPRs: permlane swaps across rows or halves, DPP within
+                    // a row (only lanes below half use them)
+                    float up, own;
+                    if (A.tr == 64) pair_of<true>(v[m], own, up);
+                    else if (A.tr == 32) pair_of<false>(v[m], own, up);
+                    else up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[m]),
+                                                                                     0x128, 0xf, 0xf, false));   // row_ror:8
                     const float g = v[m];
                     const uint32_t act = f2h(g / (1.0f + expf(-g)) * up);
-                    const uint32_t next = __shfl_down(act, 1, 64);
+                    const uint32_t next = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)act, 0x101, 0xf, 0xf, false);   // row_shl:1
                     if (lane < half && (lane & 1) == 0 && j < In)
                         put(a.act + (size_t)m * (In / 2) + j / 2, act | (next << 16), tag);
                 }
@@ -1024,10 +1054,8 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
                         if (isnan(x)) x = -INFINITY;
                     }
                     Best bst = live ? Best{x, r} : Best{-INFINITY, 0x7fffffff};
-#pragma unroll
-                    for (int o = 32; o > 0; o >>= 1)
-                        bst = better(bst, Best{__shfl_xor(bst.v, o, 64), __shfl_xor(bst.i, o, 64)});
-                    bad = (int)wave_sum((float)bad);
+                    bst = wave_best(bst);
+                    bad = (int)wave_total((float)bad);
                     if (lane == 0) {
                         u64* w = a.best + ((size_t)m * A.tiles + t) * 3;
                         put(w, fbits(bst.v), tag);
@@ -1483,10 +1511,21 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         u64* out = a.attn_out + (size_t)m * kq + (size_t)g * GH;
         for (int k = tid; k < ne; k += kThreads) {
             const int h = (e0 + k) / HD;
-            // four interleaved partial sums (independent LDS loads), added in
-            // a fixed order
+            // four interleaved partial sums (split sp into sum sp % 4), added
+            // in a fixed order; four splits' LDS loads issued together
             float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            for (int sp = 0; sp < Sm; ++sp) o4[sp & 3] += vals[k * Sm + sp] * mlv[(sp * G + h) * 2];
+            int sp = 0;
+            for (; sp + 4 <= Sm; sp += 4) {
+                float v4[4], w4[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    v4[j] = vals[k * Sm + sp + j];
+                    w4[j] = mlv[((sp + j) * G + h) * 2];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o4[j] += v4[j] * w4[j];
+            }
+            for (; sp < Sm; ++sp) o4[sp & 3] += vals[k * Sm + sp] * mlv[(sp * G + h) * 2];
             const float o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
             put(&out[e0 + k], fbits(o / lsum[h]), tag);
         }
@@ -1579,9 +1618,8 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
             good = spin(a, pending) && good;
         }
         if (block_any(!good)) return;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) bst = better(bst, Best{__shfl_xor(bst.v, o, 64), __shfl_xor(bst.i, o, 64)});
-        bad = (int)wave_sum((float)bad);
+        bst = wave_best(bst);
+        bad = (int)wave_total((float)bad);
         if (lane == 0) { bv[wave] = bst.v; bi[wave] = bst.i; bb[wave] = bad; }
         __syncthreads();
         if (tid == 0) {
