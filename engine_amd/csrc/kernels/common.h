@@ -123,6 +123,18 @@ __device__ __forceinline__ float dpp_add(float v) {
 // row (after each, the lanes a rotation pairs hold equal bits), then the
 // row pairs and halves through the permlane swaps. Every lane gets the same
 // bits; the order is fixed. Every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false)));
+}
+// Maximum over the wave without LDS (exact in any order), in every lane.
+__device__ __forceinline__ float wave_top(float v) {
+    v = dpp_max<0x128>(v);   // row_ror:8
+    v = dpp_max<0x124>(v);   // row_ror:4
+    v = dpp_max<0x122>(v);   // row_ror:2
+    v = dpp_max<0x121>(v);   // row_ror:1
+    return pair32_max(pair16_max(v));
+}
 __device__ __forceinline__ float wave_total(float v) {
     v = dpp_add<0x128>(v);   // row_ror:8
     v = dpp_add<0x124>(v);   // row_ror:4

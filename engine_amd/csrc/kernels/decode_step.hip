@@ -1501,7 +1501,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         for (int h = wave; h < G; h += kWaves) {
             const bool live = lane < Sm;
             const float ms = live ? mlv[(lane * G + h) * 2] : -INFINITY;
-            const float mx = wave_max(ms);
+            const float mx = wave_top(ms);
             const float es = live ? expf(ms - mx) : 0.0f;
             const float L = wave_total(live ? mlv[(lane * G + h) * 2 + 1] * es : 0.0f);
             if (live) mlv[(lane * G + h) * 2] = es;
