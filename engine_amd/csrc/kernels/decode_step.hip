@@ -201,6 +201,11 @@ __device__ __forceinline__ void mark(const StepArgs& a, int ph, int kind) {
 // reads the workgroup size from the dispatch packet with a vector load; the
 // wait for it also waits for every load issued before, prefetched weight
 // chunks included.)
+// Each call site (Site) has its own votes, so one barrier suffices: a wave
+// rewrites a site's votes only at that site's next call, and a barrier lies
+// between any two calls of one site, which every wave reaches only once it
+// has read the votes.
+template <int Site>
 __device__ __forceinline__ bool block_any(bool x) {
     __shared__ uint32_t votes[kWaves];
     const int t = threadIdx.x;
@@ -210,12 +215,12 @@ __device__ __forceinline__ bool block_any(bool x) {
     uint32_t r = 0;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) r |= votes[i];
-    __syncthreads();   // the votes are rewritten by the next call
     return r != 0;
 }
 
 // Sum of v over the workgroup for M rows; every thread gets the sums. Waves
-// are added in wave order.
+// are added in wave order. One barrier: the caller (the RMSNorm window) is
+// followed by a barrier before any next call rewrites the partials.
 template <int M>
 __device__ __forceinline__ void block_sum_rows(float (&v)[M], int tid) {
     __shared__ float part[kWaves][kMaxRows];
@@ -233,7 +238,6 @@ __device__ __forceinline__ void block_sum_rows(float (&v)[M], int tid) {
         for (int w = 0; w < kWaves; ++w) s += part[w][m];
         v[m] = s;
     }
-    __syncthreads();
 }
 
 // ------------------------------------------------------------ GEMV phase
@@ -801,7 +805,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     if (g0 + 1 < w1) CM::load(A, g0 + 1, nv_of(g0 + 1), lane, wb, sb);
     const bool ok = spin(a, attempt);
     // one decision for the workgroup before any code with barriers
-    if (block_any(!ok)) return false;
+    if (block_any<0>(!ok)) return false;
     if (normed) {
         if (d) rin.apply(h, H, tid);
         if (p.busy) norm_window<M, Q8>(a, h, gv, A, p, xs, tid);
@@ -1067,7 +1071,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
             }
         }
     }
-    if (block_any(!good)) return false;
+    if (block_any<1>(!good)) return false;
     mark(a, ph, 3);
     return true;
 }
@@ -1292,7 +1296,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 }
             }
         }
-        if (block_any(!ok)) return false;
+        if (block_any<2>(!ok)) return false;
         // RoPE on q (every head, split into fp16 parts) and on the current
         // key, from the host-built cos/sin tables
         {
@@ -1495,7 +1499,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 else if (e < nw) vals[e - nml] = bitsf(v[u2]);
             }
         }
-        if (block_any(!ok)) return false;
+        if (block_any<3>(!ok)) return false;
         // split weights e_s = exp(m_s - max) and the total sum, one wave per
         // head and a lane per split (splits <= 64)
         for (int h = wave; h < G; h += kWaves) {
@@ -1617,7 +1621,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
             auto pending = [&]() { return load_sc1(a.seq + w) == seq + 1u ? 0 : 1; };
             good = spin(a, pending) && good;
         }
-        if (block_any(!good)) return;
+        if (block_any<4>(!good)) return;
         bst = wave_best(bst);
         bad = (int)wave_total((float)bad);
         if (lane == 0) { bv[wave] = bst.v; bi[wave] = bst.i; bb[wave] = bad; }
