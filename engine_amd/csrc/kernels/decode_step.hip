@@ -324,6 +324,63 @@ __device__ __forceinline__ Part partition(const Mat& A, int G) {
     return p;
 }
 
+// The shapes of the five GEMV phases' matrices (qkv, o, gate/up, down, LM
+// head: the phase slots) and this workgroup's share of each, computed once
+// per launch into LDS by geo_init: make_mat and partition divide by run-time
+// values (a VALU division is ~25 ops), and done at every phase entry they
+// sat on the critical path of the workgroups that finish a phase last.
+struct Geo {
+    int n, k, tr, lpr, tiles, nb, chunks, ck;
+    int f0, f1, pieces, gp, ca, win, busy;
+};
+__device__ __forceinline__ Geo* geo_table() {
+    __shared__ Geo geo[5];
+    return geo;
+}
+template <bool Q8>
+__device__ __forceinline__ void geo_init(const StepArgs& a) {
+    const int i = threadIdx.x;
+    if (i < 5) {
+        const int H = a.md.hidden_size, nq = a.md.num_heads, nkv = a.md.num_kv_heads, hd = a.md.head_dim;
+        const int In = a.md.intermediate_size, V = a.md.vocab_size;
+        const int n = i == 0 ? (nq + 2 * nkv) * hd : i == 1 || i == 3 ? H : i == 2 ? In : V;
+        const int k = i == 1 ? nq * hd : i == 3 ? In : H;
+        const Mat A = make_mat<Q8>(nullptr, nullptr, n, k, i == 2, a.md.tile_rows[i]);
+        const Part p = partition(A, i == 1 ? a.o_grid : (int)gridDim.x);
+        geo_table()[i] = Geo{A.n, A.k, A.tr, A.lpr, A.tiles, A.nb, A.chunks, A.ck,
+                             p.f0, p.f1, p.pieces, p.gp, p.ca, p.win, p.busy ? 1 : 0};
+    }
+}
+// Slot i's matrix over the given weights and scales, and this workgroup's
+// share (wave-uniform values, kept in SGPRs).
+__device__ __forceinline__ Mat geo_mat(int i, const void* w, const void* s) {
+    const Geo& g = geo_table()[i];
+    Mat m;
+    m.w = static_cast<const u32x4*>(w);
+    m.s = s;
+    m.n = uniform(g.n);
+    m.k = uniform(g.k);
+    m.tr = uniform(g.tr);
+    m.lpr = uniform(g.lpr);
+    m.tiles = uniform(g.tiles);
+    m.nb = uniform(g.nb);
+    m.chunks = uniform(g.chunks);
+    m.ck = uniform(g.ck);
+    return m;
+}
+__device__ __forceinline__ Part geo_part(int i) {
+    const Geo& g = geo_table()[i];
+    Part p;
+    p.f0 = uniform(g.f0);
+    p.f1 = uniform(g.f1);
+    p.pieces = uniform(g.pieces);
+    p.gp = uniform(g.gp);
+    p.ca = uniform(g.ca);
+    p.win = uniform(g.win);
+    p.busy = uniform(g.busy) != 0;
+    return p;
+}
+
 // Accumulates one chunk of the matrix into acc (x from the LDS window).
 template <int M, bool Q8>
 struct ChunkMath;
@@ -500,9 +557,8 @@ template <bool Q8>
 __device__ __forceinline__ void stage_gateup(const StepArgs& a, const lyk_step_layer& Lw) {
     if (a.pf_chunks == 0) return;
     extern __shared__ __align__(16) unsigned char smem[];
-    const Mat A = make_mat<Q8>(Lw.gateup_w, Lw.gateup_s, a.md.intermediate_size, a.md.hidden_size, true,
-                               a.md.tile_rows[2]);
-    const Part p = partition(A, gridDim.x);
+    const Mat A = geo_mat(2, Lw.gateup_w, Lw.gateup_s);
+    const Part p = geo_part(2);
     if (!p.busy) return;
     const int tid = phase_tid();
     const int lane = tid & 63, wave = uniform(tid >> 6);
@@ -722,20 +778,19 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     const uint32_t tag = tag0 | (uint32_t)l;   // l == L for the LM head
     const void* wp;
     const void* sp;
-    int n, k;
     switch (kind) {
-        case kQkv: wp = Lw.qkv_w; sp = Lw.qkv_s; n = rows; k = H; break;
-        case kOut: wp = Lw.o_w; sp = Lw.o_s; n = H; k = nq * hd; break;
-        case kGateUp: wp = Lw.gateup_w; sp = Lw.gateup_s; n = In; k = H; break;
-        case kDown: wp = Lw.down_w; sp = Lw.down_s; n = H; k = In; break;
-        default: wp = a.md.lm_head_w; sp = a.md.lm_head_s; n = V; k = H; break;
+        case kQkv: wp = Lw.qkv_w; sp = Lw.qkv_s; break;
+        case kOut: wp = Lw.o_w; sp = Lw.o_s; break;
+        case kGateUp: wp = Lw.gateup_w; sp = Lw.gateup_s; break;
+        case kDown: wp = Lw.down_w; sp = Lw.down_s; break;
+        default: wp = a.md.lm_head_w; sp = a.md.lm_head_s; break;
     }
     // matrices of a phase kind share a slot: qkv 0, o 1, gate/up 2, down 3, head 4
     const int slot = kind == kQkv ? 0 : kind - 1;
-    const Mat A = make_mat<Q8>(wp, sp, n, k, kind == kGateUp, a.md.tile_rows[slot]);
+    const Mat A = geo_mat(slot, wp, sp);
     const int CK = A.ck;
     mark(a, ph, 0);
-    const Part p = partition(A, kind == kOut ? a.o_grid : (int)gridDim.x);
+    const Part p = geo_part(slot);
     const int b = blockIdx.x;
     const int lane = tid & 63, wave = uniform(tid >> 6);
     const int len = p.f1 - p.f0;
@@ -1568,6 +1623,9 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(const StepArgs* _
             }
         }
     }
+
+    geo_init<Q8>(a);
+    __syncthreads();   // the phase geometry is in LDS before any phase reads it
 
     // per layer: QKV, attention, O, gate/up, down; then the LM head
     const int nph = 5 * L + (a.io.mode == LYK_STEP_HIDDEN ? 0 : 1);
