@@ -332,7 +332,21 @@ __device__ __forceinline__ Part partition(const Mat& A, int G) {
 struct Geo {
     int n, k, tr, lpr, tiles, nb, chunks, ck;
     int f0, f1, pieces, gp, ca, win, busy;
+    uint32_t cmag;   // x / chunks == (x * cmag) >> csh for 0 <= x < 2^24
+    int csh;
 };
+// Granlund-Montgomery reciprocal of d (1 <= d < 2^24) for 24-bit dividends:
+// l = ceil(log2 d), m = floor(2^(24+l) / d) + 1 < 2^26; then m*d lies in
+// (2^(24+l), 2^(24+l) + 2^l], which makes floor(x*m / 2^(24+l)) == x / d.
+__host__ __device__ __forceinline__ void recip24(int d, uint32_t& m, int& sh) {
+    int l = 0;
+    while ((1 << l) < d) ++l;
+    sh = 24 + l;
+    m = (uint32_t)((1ull << sh) / (uint64_t)d + 1);
+}
+__device__ __forceinline__ int div24(int x, uint32_t m, int sh) {
+    return (int)(((uint64_t)(uint32_t)x * m) >> sh);
+}
 __device__ __forceinline__ Geo* geo_table() {
     __shared__ Geo geo[5];
     return geo;
@@ -347,8 +361,11 @@ __device__ __forceinline__ void geo_init(const StepArgs& a) {
         const int k = i == 1 ? nq * hd : i == 3 ? In : H;
         const Mat A = make_mat<Q8>(nullptr, nullptr, n, k, i == 2, a.md.tile_rows[i]);
         const Part p = partition(A, i == 1 ? a.o_grid : (int)gridDim.x);
+        uint32_t cm;
+        int cs;
+        recip24(A.chunks, cm, cs);
         geo_table()[i] = Geo{A.n, A.k, A.tr, A.lpr, A.tiles, A.nb, A.chunks, A.ck,
-                             p.f0, p.f1, p.pieces, p.gp, p.ca, p.win, p.busy ? 1 : 0};
+                             p.f0, p.f1, p.pieces, p.gp, p.ca, p.win, p.busy ? 1 : 0, cm, cs};
     }
 }
 // Slot i's matrix over the given weights and scales, and this workgroup's
@@ -791,6 +808,11 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     const int CK = A.ck;
     mark(a, ph, 0);
     const Part p = geo_part(slot);
+    // tile of a chunk index: x / A.chunks by the phase's reciprocal (chunk
+    // indices stay far below 2^24)
+    const uint32_t cmag = uniform((int)geo_table()[slot].cmag);
+    const int csh = uniform(geo_table()[slot].csh);
+    auto tile_of = [&](int f) { return div24(f, cmag, csh); };
     const int b = blockIdx.x;
     const int lane = tid & 63, wave = uniform(tid >> 6);
     const int len = p.f1 - p.f0;
@@ -798,7 +820,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     // valid blocks of chunk f: all but in a tile's last chunk when the tile's
     // blocks do not fill it
     const int tail = A.nb - (A.chunks - 1) * kChunkBlocks;
-    auto nv_of = [&](int f) { return tail == kChunkBlocks || (f + 1) % A.chunks ? kChunkBlocks : tail; };
+    auto nv_of = [&](int f) { return tail == kChunkBlocks || f + 1 != (tile_of(f) + 1) * A.chunks ? kChunkBlocks : tail; };
     // gate/up: the wave's chunks [w0, w0 + npf) wait in LDS (stage_gateup);
     // the register pipeline starts after them
     const int npf = kind == kGateUp ? min(a.pf_chunks, w1 - w0) : 0;
@@ -894,7 +916,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
 
     // ---- stream
     // this lane's unit within a block, and the distance between blocks, in x
-    const int usub = lane / A.tr;
+    const int usub = lane >> (A.tr == 16 ? 4 : A.tr == 32 ? 5 : 6);   // tr: 16, 32 or 64
     const int xsub = usub * CM::kUnit, xstep = A.lpr * CM::kUnit;
     float accq[kPieces][M];
 #pragma unroll
@@ -904,7 +926,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
 
     if (w0 < w1) {
         int f = w0;
-        int t = f / A.chunks;
+        int t = tile_of(f);
         int c = f - t * A.chunks;
         int q = 0;
         float acc[M];
@@ -973,8 +995,8 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     // each wave's tile sums, and the tiles [first, last] its range touched
     __shared__ int span[kWaves][2];
     {
-        const int tf = w0 < w1 ? w0 / A.chunks : 0;
-        const int tl = w0 < w1 ? (w1 - 1) / A.chunks : -1;
+        const int tf = w0 < w1 ? tile_of(w0) : 0;
+        const int tl = w0 < w1 ? tile_of(w1 - 1) : -1;
         if (lane == 0) {
             span[wave][0] = tf;
             span[wave][1] = tl;
@@ -988,7 +1010,7 @@ __device__ __forceinline__ bool gemv_step(const StepArgs& a, int ph, int kind, i
     __syncthreads();
 
     // ---- finish the workgroup's tiles, one wave per tile
-    const int tA = p.f0 / A.chunks, tB = (p.f1 - 1) / A.chunks;
+    const int tA = tile_of(p.f0), tB = tile_of(p.f1 - 1);   // busy: f1 >= 1
     const bool greedy = a.io.mode == LYK_STEP_GREEDY;
     // a region per GEMV kind: the kinds of one layer share tags
     u64* dpart = a.dpart + (size_t)(kind == kQkv ? 0 : kind - 1) * a.dpart_stride;
