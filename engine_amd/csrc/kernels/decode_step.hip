@@ -347,6 +347,16 @@ __host__ __device__ __forceinline__ void recip24(int d, uint32_t& m, int& sh) {
 __device__ __forceinline__ int div24(int x, uint32_t m, int sh) {
     return (int)(((uint64_t)(uint32_t)x * m) >> sh);
 }
+// x / d for 0 <= x < 2^20, 1 <= d < 2^12, through the hardware fp32
+// reciprocal: x * rcp(d) is within 1/8 of x / d (relative error below
+// 2^-22), so its truncation is off by at most one, which one comparison each
+// way corrects. A few VALU ops instead of an integer division's ~25.
+__device__ __forceinline__ int sdiv(int x, int d) {
+    int q = (int)((float)x * __builtin_amdgcn_rcpf((float)d));
+    if (q * d > x) --q;
+    else if ((q + 1) * d <= x) ++q;
+    return q;
+}
 __device__ __forceinline__ Geo* geo_table() {
     __shared__ Geo geo[5];
     return geo;
@@ -1246,8 +1256,8 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
                 Tm = T[mm];
                 ctx = ctxs[mm];
             }
-        g = r / Sm;
-        s = r % Sm;
+        g = sdiv(r, Sm);
+        s = r - g * Sm;
     };
     // units go to the workgroups from the top of the grid down: the QKV
     // tiles fill the grid from the bottom, so the first units land on
@@ -1399,11 +1409,12 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         __syncthreads();
         if (last) {
             // the current row into the cache: K row-major, V transposed
-            const int blk = ld(tab + pos / bt);
+            const int pb = bt_log >= 0 ? pos >> bt_log : pos / bt, ps = pos - pb * bt;
+            const int blk = ld(tab + pb);
             const size_t base = (size_t)blk * blk_stride + (size_t)g * head_stride;
             for (int i = tid; i < HD; i += kThreads) {
-                store_sc1_u16(Lw.k_cache + base + (size_t)(pos % bt) * HD + i, kcur[i]);
-                store_sc1_u16(Lw.v_cache + base + (size_t)i * bt + pos % bt, vcur[i]);
+                store_sc1_u16(Lw.k_cache + base + (size_t)ps * HD + i, kcur[i]);
+                store_sc1_u16(Lw.v_cache + base + (size_t)i * bt + ps, vcur[i]);
             }
         }
         if (u == rb) mark(a, ph, 1);
@@ -1545,7 +1556,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         unit_of(u, m, g, s, Sm, Tm, ctx);
         if (Sm == 1) continue;
         const size_t grp = (size_t)m * nkv + g;
-        const int E = (GH + Sm - 1) / Sm, e0 = s * E, ne = max(0, min(GH, e0 + E) - e0);
+        const int E = sdiv(GH + Sm - 1, Sm), e0 = s * E, ne = max(0, min(GH, e0 + E) - e0);
         float* mlv = sc;                                // [Sm][G][2] max, sum -> weight, sum
         float* vals = sc + kAttnMaxSplits * 16 * 2;     // [ne][Sm]
         __shared__ float lsum[16];
@@ -1553,9 +1564,12 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, int ph, const
         for (int b0 = tid; b0 < nw; b0 += kThreads * 4) {
             uint32_t v[4];
             auto word = [&](int e) -> const u64* {
-                if (e < nml) return a.attn_ml + (grp * kAttnMaxSplits + e / (2 * G)) * G * 2 + e % (2 * G);
-                const int k = e - nml;
-                return a.attn_acc + (grp * kAttnMaxSplits + k % Sm) * (size_t)GH + e0 + k / Sm;
+                if (e < nml) {
+                    const int sp = sdiv(e, 2 * G);
+                    return a.attn_ml + (grp * kAttnMaxSplits + sp) * G * 2 + (e - sp * 2 * G);
+                }
+                const int k = e - nml, kq2 = sdiv(k, Sm);
+                return a.attn_acc + (grp * kAttnMaxSplits + (k - kq2 * Sm)) * (size_t)GH + e0 + kq2;
             };
             uint32_t want = 0, have = 0;
             const u64* at[4];   // the words' addresses, once for every attempt
